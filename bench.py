@@ -1,0 +1,246 @@
+#!/usr/bin/env python3
+"""Benchmark of the HTile hot path on one MI355X.
+
+Default workload (the configuration BASELINE.json's metric is quoted on,
+configs[1]): causal bf16 prefill flash-attention B=4 H=32 S=4096 D=128 with
+per-row logsumexp, inputs ~ 0.5 N(0,1) resident in HBM. A step is one
+neptune_attn_fwd launch over that batch. The JSON line also carries, under
+"secondary", the split-K GQA decode (bf16 and fp8 KV) and selective-scan
+configurations measured the same way (GB/s against HBM).
+
+roofline.achieved = algorithmic FLOPs (or bytes) per launch / mean launch
+duration from HIP events on the launch stream; cpu_baseline = the CPU oracle
+(oracle/, OpenMP) on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT, ROOT / "mlir-toy_amd"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+METRIC = "attention TFLOP/s (% MFMA peak); decode/scan GB/s (% HBM peak), 1 GPU"
+PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/clk/CU
+PEAK_HBM_GBS = 8000.0       # HBM3E
+
+
+def prefill_flops(B, H, S, D):
+    # exact count of unmasked (query, key) pairs under the causal mask, two
+    # GEMMs of 2*D FLOPs each per pair
+    return 4.0 * B * H * D * S * (S + 1) / 2
+
+
+def time_launches(fn, steps, warmup, rotate=1):
+    """Run warmup + steps launches; returns (wall seconds for the timed
+    steps, mean per-launch seconds from HIP events on the current stream)."""
+    import torch
+
+    for i in range(warmup):
+        fn(i % rotate)
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    stops = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        fn(i % rotate)
+        stops[i].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev = sum(a.elapsed_time(b) for a, b in zip(starts, stops)) / steps / 1e3
+    return wall, ev
+
+
+def bench_prefill(ops, torch, steps, warmup, B=4, H=32, S=4096, D=128):
+    g = torch.Generator(device="cuda").manual_seed(2)
+    q, k, v = (torch.randn((B, H, S, D), device="cuda", generator=g).mul_(0.5).to(torch.bfloat16)
+               for _ in range(3))
+    out = torch.empty_like(q)
+    lse = torch.empty((B, H, S), dtype=torch.float32, device="cuda")
+
+    def step(_):
+        ops.attention(q, k, v, causal=True, out=out, lse=lse)
+
+    wall, ev = time_launches(step, steps, warmup)
+    flops = prefill_flops(B, H, S, D)
+    return {"q": q, "k": k, "v": v, "wall": wall, "event_s": ev, "flops": flops}
+
+
+def bench_decode(ops, torch, steps, warmup, fp8):
+    B, Hq, Hk, L, D, splits = 16, 32, 8, 32768, 128, 16
+    g = torch.Generator(device="cuda").manual_seed(3)
+    q = torch.randn((B, Hq, D), device="cuda", generator=g).to(torch.bfloat16)
+    k = torch.randn((B, Hk, L, D), device="cuda", generator=g).to(torch.bfloat16)
+    v = torch.randn((B, Hk, L, D), device="cuda", generator=g).to(torch.bfloat16)
+    ks = vs = None
+    if fp8:
+        k, ks = ops.kv_quantize_fp8(k)
+        v, vs = ops.kv_quantize_fp8(v)
+    ws = torch.empty(ops.decode_workspace_bytes(q, k, num_splits=splits, fp8=fp8),
+                     dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+
+    def step(_):
+        ops.decode_splitk(q, k, v, k_scale=ks, v_scale=vs, num_splits=splits, workspace=ws)
+
+    wall, ev = time_launches(step, steps, warmup)
+    kv_bytes = 2 * B * Hk * L * D * (1 if fp8 else 2)
+    scale_bytes = 2 * B * Hk * (L // 64) * 4 if fp8 else 0
+    nbytes = kv_bytes + scale_bytes + 2 * B * Hq * D * 2
+    name = "config5 fp8-KV split-K GQA decode" if fp8 else "config3 bf16 split-K GQA decode"
+    return name, wall, ev, nbytes
+
+
+def bench_scan(ops, torch, steps, warmup, rotate=2):
+    Bn, L, Dm, N = 4, 2048, 5120, 16
+    sets = []
+    for r in range(rotate):
+        g = torch.Generator(device="cuda").manual_seed(100 + r)
+
+        def rn(shape, dtype=torch.bfloat16):
+            return torch.randn(shape, device="cuda", generator=g).to(dtype)
+
+        u, dr, z = rn((Bn, Dm, L)), rn((Bn, Dm, L)), rn((Bn, Dm, L))
+        Bm, Cm = rn((Bn, N, L)), rn((Bn, N, L))
+        A = -torch.exp(rn((Dm, N), torch.float32))
+        Dv, bias = rn((Dm,), torch.float32), rn((Dm,), torch.float32)
+        sets.append((u, dr, A, Bm, Cm, Dv, z, bias))
+
+    def step(i):
+        ops.selective_scan(*sets[i])
+
+    wall, ev = time_launches(step, steps, warmup, rotate)
+    nbytes = 4 * Bn * Dm * L * 2 + 2 * Bn * N * L * 2 + Dm * N * 4 + 2 * Dm * 4
+    return "config4 Mamba-1 selective scan", wall, ev, nbytes
+
+
+def cpu_baseline_prefill(res, budget_s=15.0, max_heads=32):
+    """CPU oracle (HTile policy, OpenMP) on whole (batch 0, head h) slices of
+    the same inputs until the time budget is spent."""
+    import numpy as np
+    import torch
+
+    import oracle
+
+    S, D = res["q"].shape[2], res["q"].shape[3]
+    per_head = prefill_flops(1, 1, S, D)
+
+    def b16(t):
+        return t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+    done, elapsed = 0, 0.0
+    while elapsed < budget_s and done < max_heads:
+        h = done
+        sl = (slice(0, 1), slice(h, h + 1))
+        qs, ks, vs = b16(res["q"][sl]), b16(res["k"][sl]), b16(res["v"][sl])
+        t0 = time.perf_counter()
+        oracle.attn_fwd(qs, ks, vs, oracle.BF16, causal=True)
+        elapsed += time.perf_counter() - t0
+        done += 1
+    return {
+        "value": per_head * done / elapsed / 1e12,
+        "unit": "TFLOP/s",
+        "cores": oracle.num_threads(),
+        "kind": "port",
+        "sample": f"{done} of 128 (batch, head) slices of the same causal prefill "
+                  f"({elapsed:.1f} s of CPU oracle time)",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the decode/scan configurations")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this backend runs on one GPU; multi-GPU sharding is a "
+                          "design note only (no collectives are built)", "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import torch
+
+    from neptune_hip import ops
+
+    torch.cuda.set_device(0)
+    arch = torch.cuda.get_device_properties(0).gcnArchName
+    print(f"# device {torch.cuda.get_device_name(0)} {arch}", file=sys.stderr, flush=True)
+
+    res = bench_prefill(ops, torch, args.steps, args.warmup)
+    value = res["flops"] * args.steps / res["wall"] / 1e12
+    achieved = res["flops"] / res["event_s"] / 1e12
+    print(f"# prefill done: {res['event_s'] * 1e6:.1f} us/launch, {achieved:.1f} TFLOP/s",
+          file=sys.stderr, flush=True)
+
+    secondary = []
+    if not args.no_secondary:
+        del res["k"], res["v"]
+        torch.cuda.empty_cache()
+        sec_steps, sec_warm = min(args.steps, 20), min(args.warmup, 3)
+        for fn in (lambda: bench_decode(ops, torch, sec_steps, sec_warm, fp8=False),
+                   lambda: bench_decode(ops, torch, sec_steps, sec_warm, fp8=True),
+                   lambda: bench_scan(ops, torch, sec_steps, sec_warm)):
+            name, wall, ev, nbytes = fn()
+            gbs = nbytes / ev / 1e9
+            secondary.append({
+                "workload": name,
+                "value": round(nbytes * sec_steps / wall / 1e9, 1),
+                "unit": "GB/s",
+                "us_per_step": round(ev * 1e6, 2),
+                "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                             "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                             "traffic": None},
+            })
+            print(f"# {name}: {ev * 1e6:.1f} us, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
+            torch.cuda.empty_cache()
+        # the prefill inputs are still needed for the CPU sample
+        g = torch.Generator(device="cuda").manual_seed(2)
+        shape = res["q"].shape
+        res["q"], res["k"], res["v"] = (
+            torch.randn(shape, device="cuda", generator=g).mul_(0.5).to(torch.bfloat16)
+            for _ in range(3))
+
+    cpu = None if args.no_cpu else cpu_baseline_prefill(res)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["wall"] / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "config2 causal prefill flash-attention bf16 in / fp32 "
+                               "accumulate, output bf16 + per-row LSE fp32",
+                   "batch": 4, "heads": 32, "seq_len": 4096, "head_dim": 128,
+                   "causal": True, "flops_per_step": res["flops"]},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

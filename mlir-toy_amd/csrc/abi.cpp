@@ -1,0 +1,292 @@
+// abi.cpp — the extern "C" entry points of libneptune_hip.so
+// (declared in include/neptune_hip.h).
+//
+// Every request is validated on the host before any HIP call, so argument
+// errors are reported identically with or without a GPU. Failures return a
+// status code and leave a message for neptune_last_error() on the calling
+// thread; no C++ exception crosses the boundary. The reference reports the
+// same classes of failure as RuntimeError (toolchain/runtime failure,
+// src/neptune_mlir/translators/common.py:217-224) and NotImplementedError
+// (valid input outside what the backend covers, common.py:187-197).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/neptune_hip.h"
+#include "kernels.h"
+
+using namespace neptune;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+neptune_status fail(neptune_status st, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return st;
+}
+
+neptune_status ok() {
+  g_last_error.clear();
+  return NEPTUNE_OK;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Resolve (batch, head, seq) strides; all-zero means contiguous.
+bool resolve_strides(const int64_t in[3], int64_t heads, int64_t seq, int64_t dim,
+                     int64_t out[3]) {
+  if (in[0] == 0 && in[1] == 0 && in[2] == 0) {
+    out[2] = dim;
+    out[1] = seq * dim;
+    out[0] = heads * seq * dim;
+    return true;
+  }
+  for (int i = 0; i < 3; ++i) {
+    if (in[i] <= 0) return false;
+    out[i] = in[i];
+  }
+  return true;
+}
+
+neptune_status device_ready() {
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n <= 0)
+    return fail(NEPTUNE_ERR_NO_DEVICE, "no HIP device available (%s)",
+                e == hipSuccess ? "device count is 0" : hipGetErrorString(e));
+  return NEPTUNE_OK;
+}
+
+neptune_status hip_result(hipError_t e, const char *what) {
+  if (e != hipSuccess)
+    return fail(NEPTUNE_ERR_HIP, "%s: HIP error %d (%s)", what, (int)e, hipGetErrorString(e));
+  return ok();
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Split layout; identical rule in the CPU oracle (neptune_cpu_decode_layout).
+void decode_layout(const neptune_decode_desc *d, int64_t *splits, int64_t *chunk) {
+  int64_t want = d->num_splits;
+  if (want <= 0) {
+    int64_t groups = d->batch * d->heads_kv;
+    want = cdiv(2048, groups);
+    int64_t cap = cdiv(d->seq_kv, 256);
+    if (want > cap) want = cap;
+    if (want < 1) want = 1;
+  }
+  int64_t c = cdiv(cdiv(d->seq_kv, want), 64) * 64;
+  *chunk = c;
+  *splits = cdiv(d->seq_kv, c);
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+neptune_status decode_check(const neptune_decode_desc *d) {
+  if (!d) return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode: desc is NULL");
+  if (d->batch <= 0 || d->heads_q <= 0 || d->heads_kv <= 0 || d->seq_kv <= 0 ||
+      d->head_dim <= 0 || d->num_splits < 0 || d->scale_block < 0)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT,
+                "decode: sizes must be positive (batch=%lld heads_q=%lld heads_kv=%lld "
+                "seq_kv=%lld head_dim=%lld num_splits=%lld)",
+                (long long)d->batch, (long long)d->heads_q, (long long)d->heads_kv,
+                (long long)d->seq_kv, (long long)d->head_dim, (long long)d->num_splits);
+  if (d->heads_q % d->heads_kv)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode: heads_q (%lld) %% heads_kv (%lld) != 0",
+                (long long)d->heads_q, (long long)d->heads_kv);
+  if (d->q_dtype != NEPTUNE_DTYPE_BF16)
+    return fail(NEPTUNE_ERR_UNSUPPORTED, "decode: q_dtype must be BF16");
+  if (d->kv_dtype != NEPTUNE_DTYPE_BF16 && d->kv_dtype != NEPTUNE_DTYPE_FP8_E4M3)
+    return fail(NEPTUNE_ERR_UNSUPPORTED, "decode: kv_dtype must be BF16 or FP8_E4M3");
+  if (!(d->scale_log2 >= 0.0f) || !std::isfinite(d->scale_log2))
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode: scale_log2 must be finite and >= 0");
+  return NEPTUNE_OK;
+}
+
+size_t decode_ws_bytes(const neptune_decode_desc *d, int64_t splits) {
+  size_t rows = (size_t)d->batch * d->heads_q * splits;
+  return align256(rows * d->head_dim * 4) + align256(rows * 2 * 4);
+}
+
+}  // namespace
+
+extern "C" {
+
+neptune_status neptune_hip_get_backend_info(neptune_backend_info *info) {
+  if (!info) return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "info is NULL");
+  info->abi_version = NEPTUNE_HIP_ABI_VERSION;
+  info->name = "NeptuneHTileHIP";
+  info->gcn_arch = "gfx950";
+  int v = -1;
+  if (hipRuntimeGetVersion(&v) != hipSuccess) v = -1;
+  info->hip_runtime_version = v;
+  return ok();
+}
+
+const char *neptune_last_error(void) { return g_last_error.c_str(); }
+
+int32_t neptune_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+neptune_status neptune_attn_fwd(const neptune_attn_desc *d, const void *q, const void *k,
+                                const void *v, void *o, float *lse, void *stream) {
+  if (!d) return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "attn_fwd: desc is NULL");
+  if (!q || !k || !v || !o)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "attn_fwd: q, k, v and o must be non-NULL");
+  if (d->batch <= 0 || d->heads_q <= 0 || d->heads_kv <= 0 || d->seq_q <= 0 ||
+      d->seq_kv <= 0 || d->head_dim <= 0)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT,
+                "attn_fwd: sizes must be positive (batch=%lld heads_q=%lld heads_kv=%lld "
+                "seq_q=%lld seq_kv=%lld head_dim=%lld)",
+                (long long)d->batch, (long long)d->heads_q, (long long)d->heads_kv,
+                (long long)d->seq_q, (long long)d->seq_kv, (long long)d->head_dim);
+  if (d->heads_q % d->heads_kv)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "attn_fwd: heads_q (%lld) %% heads_kv (%lld) != 0",
+                (long long)d->heads_q, (long long)d->heads_kv);
+  if (d->dtype != NEPTUNE_DTYPE_F32 && d->dtype != NEPTUNE_DTYPE_F16 &&
+      d->dtype != NEPTUNE_DTYPE_BF16)
+    return fail(NEPTUNE_ERR_UNSUPPORTED, "attn_fwd: dtype %d (need F32, F16 or BF16)",
+                (int)d->dtype);
+  if (!(d->scale_log2 >= 0.0f) || !std::isfinite(d->scale_log2))
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "attn_fwd: scale_log2 must be finite and >= 0");
+  AttnLaunch L;
+  L.q = q; L.k = k; L.v = v; L.o = o; L.lse = lse;
+  L.batch = d->batch; L.heads_q = d->heads_q; L.heads_kv = d->heads_kv;
+  L.seq_q = d->seq_q; L.seq_kv = d->seq_kv; L.head_dim = d->head_dim;
+  if (!resolve_strides(d->q_stride, d->heads_q, d->seq_q, d->head_dim, L.qs) ||
+      !resolve_strides(d->k_stride, d->heads_kv, d->seq_kv, d->head_dim, L.ks) ||
+      !resolve_strides(d->v_stride, d->heads_kv, d->seq_kv, d->head_dim, L.vs) ||
+      !resolve_strides(d->o_stride, d->heads_q, d->seq_q, d->head_dim, L.os))
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT,
+                "attn_fwd: strides must be all zero (contiguous) or all positive");
+  L.dtype = d->dtype;
+  L.causal = d->causal ? 1 : 0;
+  L.scale_log2 = d->scale_log2 != 0.0f
+                     ? d->scale_log2
+                     : (float)(1.4426950408889634 / std::sqrt((double)d->head_dim));
+  if (d->dtype != NEPTUNE_DTYPE_F32) {
+    bool strides8 = true;
+    for (int i = 0; i < 3; ++i)
+      strides8 = strides8 && L.qs[i] % 8 == 0 && L.ks[i] % 8 == 0 && L.vs[i] % 8 == 0 &&
+                 L.os[i] % 8 == 0;
+    if (!strides8 || !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+      return fail(NEPTUNE_ERR_UNSUPPORTED,
+                  "attn_fwd: 16-bit tensors need 16-byte aligned base pointers and strides "
+                  "that are multiples of 8 elements");
+  }
+  const char *why = "";
+  if (!attn_supported(L, &why)) return fail(NEPTUNE_ERR_UNSUPPORTED, "attn_fwd: %s", why);
+  neptune_status st = device_ready();
+  if (st != NEPTUNE_OK) return st;
+  return hip_result(launch_attn_fwd(L, (hipStream_t)stream), "attn_fwd launch");
+}
+
+neptune_status neptune_decode_workspace_bytes(const neptune_decode_desc *d, size_t *bytes) {
+  if (!bytes) return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode_workspace_bytes: bytes is NULL");
+  neptune_status st = decode_check(d);
+  if (st != NEPTUNE_OK) return st;
+  int64_t splits, chunk;
+  decode_layout(d, &splits, &chunk);
+  *bytes = decode_ws_bytes(d, splits);
+  return ok();
+}
+
+neptune_status neptune_decode_splitk(const neptune_decode_desc *d, const void *q,
+                                     const void *k, const void *v, const float *k_scale,
+                                     const float *v_scale, void *o, float *lse,
+                                     void *workspace, size_t workspace_bytes, void *stream) {
+  neptune_status st = decode_check(d);
+  if (st != NEPTUNE_OK) return st;
+  if (!q || !k || !v || !o)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode: q, k, v and o must be non-NULL");
+  const bool fp8 = d->kv_dtype == NEPTUNE_DTYPE_FP8_E4M3;
+  if (fp8 && (!k_scale || !v_scale))
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode: fp8 KV needs k_scale and v_scale");
+  if (!workspace) return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode: workspace is NULL");
+  int64_t splits, chunk;
+  decode_layout(d, &splits, &chunk);
+  const size_t need = decode_ws_bytes(d, splits);
+  if (workspace_bytes < need)
+    return fail(NEPTUNE_ERR_WORKSPACE_TOO_SMALL, "decode: workspace %zu bytes, need %zu",
+                workspace_bytes, need);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(workspace))
+    return fail(NEPTUNE_ERR_UNSUPPORTED, "decode: q, k, v and workspace must be 16-byte aligned");
+  DecodeLaunch L;
+  L.q = q; L.k = k; L.v = v; L.k_scale = k_scale; L.v_scale = v_scale;
+  L.o = o; L.lse = lse;
+  L.batch = d->batch; L.heads_q = d->heads_q; L.heads_kv = d->heads_kv;
+  L.seq_kv = d->seq_kv; L.head_dim = d->head_dim;
+  L.splits = splits; L.chunk = chunk;
+  L.scale_block = d->scale_block > 0 ? d->scale_block : 64;
+  L.n_scale_blocks = cdiv(d->seq_kv, L.scale_block);
+  L.kv_dtype = d->kv_dtype;
+  L.scale_log2 = d->scale_log2 != 0.0f
+                     ? d->scale_log2
+                     : (float)(1.4426950408889634 / std::sqrt((double)d->head_dim));
+  const size_t rows = (size_t)d->batch * d->heads_q * splits;
+  L.part_o = (float *)workspace;
+  L.part_ml = (float *)((char *)workspace + align256(rows * d->head_dim * 4));
+  const char *why = "";
+  if (!decode_supported(L, &why)) return fail(NEPTUNE_ERR_UNSUPPORTED, "decode: %s", why);
+  st = device_ready();
+  if (st != NEPTUNE_OK) return st;
+  return hip_result(launch_decode(L, (hipStream_t)stream), "decode launch");
+}
+
+neptune_status neptune_kv_quantize_fp8(int64_t batch, int64_t heads_kv, int64_t seq_kv,
+                                       int64_t head_dim, int64_t scale_block, const void *src,
+                                       uint8_t *codes, float *scales, void *stream) {
+  if (!src || !codes || !scales)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "kv_quantize: src, codes and scales must be non-NULL");
+  if (batch <= 0 || heads_kv <= 0 || seq_kv <= 0 || head_dim <= 0 || scale_block < 0)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "kv_quantize: sizes must be positive");
+  if (batch * heads_kv * cdiv(seq_kv, scale_block > 0 ? scale_block : 64) > ((int64_t)1 << 31) - 1 ||
+      seq_kv * head_dim > ((int64_t)1 << 31) - 1)
+    return fail(NEPTUNE_ERR_UNSUPPORTED, "kv_quantize: shape too large for one launch");
+  QuantLaunch L;
+  L.src = src; L.codes = codes; L.scales = scales;
+  L.batch = batch; L.heads_kv = heads_kv; L.seq_kv = seq_kv; L.head_dim = head_dim;
+  L.scale_block = scale_block > 0 ? scale_block : 64;
+  L.n_scale_blocks = cdiv(seq_kv, L.scale_block);
+  neptune_status st = device_ready();
+  if (st != NEPTUNE_OK) return st;
+  return hip_result(launch_kv_quantize(L, (hipStream_t)stream), "kv_quantize launch");
+}
+
+neptune_status neptune_selective_scan_fwd(const neptune_scan_desc *d, const void *u,
+                                          const void *delta_raw, const float *A, const void *B,
+                                          const void *C, const float *D, const void *z,
+                                          const float *delta_bias, void *y, void *stream) {
+  if (!d) return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "selective_scan: desc is NULL");
+  if (!u || !delta_raw || !A || !B || !C || !y)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT,
+                "selective_scan: u, delta, A, B, C and y must be non-NULL");
+  if (d->batch <= 0 || d->dim <= 0 || d->seq_len <= 0 || d->d_state <= 0)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "selective_scan: sizes must be positive");
+  if (d->io_dtype != NEPTUNE_DTYPE_BF16)
+    return fail(NEPTUNE_ERR_UNSUPPORTED, "selective_scan: io_dtype must be BF16");
+  ScanLaunch L;
+  L.u = u; L.delta_raw = delta_raw; L.B = B; L.C = C; L.z = z;
+  L.A = A; L.D = D; L.delta_bias = delta_bias; L.y = y;
+  L.batch = d->batch; L.dim = d->dim; L.seq_len = d->seq_len; L.d_state = d->d_state;
+  L.delta_softplus = d->delta_softplus ? 1 : 0;
+  const char *why = "";
+  if (!scan_supported(L, &why)) return fail(NEPTUNE_ERR_UNSUPPORTED, "selective_scan: %s", why);
+  neptune_status st = device_ready();
+  if (st != NEPTUNE_OK) return st;
+  return hip_result(launch_selective_scan(L, (hipStream_t)stream), "selective_scan launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,413 @@
+// attn_fwd.hip — the HTile flash-attention tile program on gfx950.
+//
+// Semantics: tests/data/flash_attention_htile.mlir:26-143 (one program per
+// (128-row query block, head, batch); K/V streamed in 64-key blocks; fp32
+// online softmax in the exp2 domain; P rounded to the 16-bit input type
+// before P.V; O = acc / l rounded on store). Additions the reference lacks:
+// causal masking (bottom-right aligned), per-row logsumexp, grouped KV heads,
+// strided tensors and ragged sequence lengths.
+//
+// MFMA formulation (16-bit inputs, v_mfma_f32_32x32x16_{bf16,f16}): each of
+// the 4 waves owns 32 query rows and computes the transposed products
+//   S^T = K · Q^T      A = K tile rows from LDS, B = Q^T held in VGPRs
+//   O^T = V^T · P^T    A = V^T from LDS,        B = P^T straight from S^T
+// so every lane holds one query row (lane % 32) in both accumulators: the
+// row max/sum are in-lane reductions plus one exchange with lane ^ 32, and
+// the rescale of O uses one per-lane factor. The K^T read order of the
+// HTile pass (dimension_order = [1,0], lib/HTile/HTilePasses.cpp:122-140)
+// is realised by the A-operand read pattern; no transpose is materialised.
+// V is transposed while it is written to LDS, with keys permuted within each
+// 16-key chunk so that the 8 keys a lane feeds to P.V (which come from the
+// 32x32 accumulator layout of S^T) are contiguous: key 8a+4g+b of a chunk is
+// stored at position 8g+4a+b.
+// K/V tiles are double-buffered in LDS (the htile.pipeline_stages = 2 hint,
+// HTile:128): the next tile's global loads are in flight while the current
+// tile is consumed, and one barrier per key block separates the phases.
+#include "device_common.h"
+#include "kernels.h"
+
+namespace neptune {
+namespace {
+
+constexpr int BM = 128;  // query rows per work-group (HTile %c128)
+constexpr int BN = 64;   // keys per block (HTile %c64)
+constexpr int NTHR = 256;
+
+struct AttnArgs {
+  const void *q, *k, *v;
+  void *o;
+  float *lse;
+  int64_t qs0, qs1, qs2, ks0, ks1, ks2, vs0, vs1, vs2, os0, os1, os2;
+  int32_t Hq, group, Sq, Sk, nqb, BH, off;  // off = Sk - Sq (causal diagonal)
+  float scale2;                             // log2(e)/sqrt(D) unless given
+};
+
+__device__ inline uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+template <class E, int D, bool CAUSAL>
+__global__ __launch_bounds__(NTHR, 2) void attn_fwd_mfma(AttnArgs a) {
+  constexpr int KP = D + 8;          // K row pitch in LDS (elements)
+  constexpr int VP = BN + 8;         // V^T row pitch in LDS (elements)
+  constexpr int KTILE = BN * KP;
+  constexpr int VTILE = D * VP;
+  constexpr int NQS = D / 16;        // MFMA k-steps over head_dim
+  constexpr int NDB = D / 32;        // 32-wide head_dim blocks of O^T
+  constexpr int CPR = D / 8;         // 16-byte chunks per row
+  constexpr int NKL = BN * CPR / NTHR;
+  constexpr int VUN = (BN / 4) * CPR;  // (4 keys x 8 dims) V units per tile
+  constexpr int NVL = (VUN + NTHR - 1) / NTHR;
+  typedef typename E::vec8 V8;
+
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (KTILE + VTILE)];
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, l = tid & 63, lq = l & 31, g = l >> 5;
+  const int id = blockIdx.x;
+  // Heaviest causal query blocks first; blocks of one (batch, head) share a
+  // residue mod 8 and hence an XCD (and its L2) whenever BH % 8 == 0.
+  const int qb = CAUSAL ? a.nqb - 1 - id / a.BH : id / a.BH;
+  const int bh = id % a.BH;
+  const int b = bh / a.Hq, h = bh % a.Hq, hk = h / a.group;
+  const uint16_t *qp = (const uint16_t *)a.q + b * a.qs0 + h * a.qs1;
+  const uint16_t *kp = (const uint16_t *)a.k + b * a.ks0 + hk * a.ks1;
+  const uint16_t *vp = (const uint16_t *)a.v + b * a.vs0 + hk * a.vs1;
+
+  const int row0 = qb * BM + w * 32;
+  const int row = row0 + lq;
+
+  u32x4 qf[NQS];
+#pragma unroll
+  for (int s = 0; s < NQS; ++s)
+    qf[s] = row < a.Sq ? *(const u32x4 *)(qp + row * a.qs2 + 16 * s + 8 * g)
+                       : u32x4{0, 0, 0, 0};
+
+  int nkb = (a.Sk + BN - 1) / BN;
+  if (CAUSAL) {
+    int last = qb * BM + BM - 1 + a.off;
+    int lim = last < 0 ? 0 : last / BN + 1;
+    nkb = nkb < lim ? nkb : lim;
+  }
+
+  u32x4 kreg[NKL];
+  u32x4 vreg[NVL][4];
+
+  auto load_tile = [&](int jb) {
+    const int key0 = jb * BN;
+#pragma unroll
+    for (int i = 0; i < NKL; ++i) {
+      int c = tid + i * NTHR, r = c / CPR, c8 = c % CPR, key = key0 + r;
+      kreg[i] = key < a.Sk ? *(const u32x4 *)(kp + key * a.ks2 + 8 * c8)
+                           : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < NVL; ++i) {
+      int u = tid + i * NTHR;
+      if (u < VUN) {
+        int kq = u / CPR, dc = u % CPR;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          int key = key0 + 4 * kq + t;
+          vreg[i][t] = key < a.Sk ? *(const u32x4 *)(vp + key * a.vs2 + 8 * dc)
+                                  : u32x4{0, 0, 0, 0};
+        }
+      }
+    }
+  };
+
+  auto store_tile = [&](int buf) {
+    uint16_t *Ks = smem + buf * (KTILE + VTILE);
+    uint16_t *Vt = Ks + KTILE;
+#pragma unroll
+    for (int i = 0; i < NKL; ++i) {
+      int c = tid + i * NTHR, r = c / CPR, c8 = c % CPR;
+      *(u32x4 *)(Ks + r * KP + 8 * c8) = kreg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < NVL; ++i) {
+      int u = tid + i * NTHR;
+      if (u < VUN) {
+        int kq = u / CPR, dc = u % CPR;
+        int pos = 16 * (kq >> 2) + 8 * (kq & 1) + 4 * ((kq >> 1) & 1);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+          u32x2 val = {perm_b32(vreg[i][1][e >> 1], vreg[i][0][e >> 1], sel),
+                       perm_b32(vreg[i][3][e >> 1], vreg[i][2][e >> 1], sel)};
+          *(u32x2 *)(Vt + (8 * dc + e) * VP + pos) = val;
+        }
+      }
+    }
+  };
+
+  f32x16 oacc[NDB];
+#pragma unroll
+  for (int nb = 0; nb < NDB; ++nb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[nb][r] = 0.0f;
+  float m = kNegFltMax, lsum = 0.0f;
+  const float sc = a.scale2;
+
+  if (nkb > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int jb = 0; jb < nkb; ++jb) {
+    const int buf = jb & 1;
+    if (jb + 1 < nkb) load_tile(jb + 1);
+    const uint16_t *Ks = smem + buf * (KTILE + VTILE);
+    const uint16_t *Vt = Ks + KTILE;
+    const int key0 = jb * BN;
+    const bool active = !CAUSAL || key0 <= row0 + 31 + a.off;
+    if (active) {
+      f32x16 s[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
+#pragma unroll
+        for (int st = 0; st < NQS; ++st) {
+          u32x4 A = *(const u32x4 *)(Ks + (32 * kb + lq) * KP + 16 * st + 8 * g);
+          s[kb] = E::mfma32(as_vec8<V8>(A), as_vec8<V8>(qf[st]), s[kb]);
+        }
+      }
+      const bool need_mask =
+          (key0 + BN > a.Sk) || (CAUSAL && key0 + BN - 1 > row0 + a.off);
+      if (need_mask) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            int key = key0 + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3);
+            if (key >= a.Sk || (CAUSAL && key > row + a.off)) s[kb][r] = -INFINITY;
+          }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+      mx = fmaxf(mx, swap_halves(mx));
+      const float m_new = fmaxf(m, mx * sc);
+      const float alpha = fast_exp2(m - m_new);
+      const float nm = -m_new;
+      float rs = 0.0f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float p = fast_exp2(fmaf(s[kb][r], sc, nm));
+          s[kb][r] = p;
+          rs += p;
+        }
+      lsum = lsum * alpha + rs;
+      m = m_new;
+      if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int nb = 0; nb < NDB; ++nb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[nb][r] *= alpha;
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int kb = c >> 1, hh = c & 1;
+        u32x4 pf;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          pf[i] = E::pack2(s[kb][8 * hh + 2 * i], s[kb][8 * hh + 2 * i + 1]);
+#pragma unroll
+        for (int nb = 0; nb < NDB; ++nb) {
+          u32x4 A = *(const u32x4 *)(Vt + (32 * nb + lq) * VP + 16 * c + 8 * g);
+          oacc[nb] = E::mfma32(as_vec8<V8>(A), as_vec8<V8>(pf), oacc[nb]);
+        }
+      }
+    }
+    if (jb + 1 < nkb) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  const float ltot = lsum + swap_halves(lsum);
+  if (row < a.Sq) {
+    uint16_t *op = (uint16_t *)a.o + b * a.os0 + h * a.os1 + row * a.os2;
+#pragma unroll
+    for (int nb = 0; nb < NDB; ++nb)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        float v4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          v4[i] = ltot > 0.0f ? oacc[nb][4 * rq + i] / ltot : 0.0f;
+        u32x2 pk = {E::pack2(v4[0], v4[1]), E::pack2(v4[2], v4[3])};
+        *(u32x2 *)(op + 32 * nb + 8 * rq + 4 * g) = pk;
+      }
+    if (g == 0 && a.lse)
+      a.lse[((int64_t)b * a.Hq + h) * a.Sq + row] =
+          ltot > 0.0f ? (m + log2f(ltot)) * kLn2 : -INFINITY;
+  }
+}
+
+// fp32 path (config 1 and any F32 request): one wave per 64 query rows,
+// one lane per row, K/V blocks staged in LDS and read as broadcasts. The
+// recurrence is the HTile one with no rounding of P (the input type is
+// fp32).
+constexpr int F32_BM = 64;
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(64) void attn_fwd_f32(AttnArgs a) {
+  __shared__ float Ks[BN][D];
+  __shared__ float Vs[BN][D];
+  const int t = threadIdx.x;
+  const int id = blockIdx.x;
+  const int qb = id / a.BH, bh = id % a.BH;
+  const int b = bh / a.Hq, h = bh % a.Hq, hk = h / a.group;
+  const float *qp = (const float *)a.q + b * a.qs0 + h * a.qs1;
+  const float *kp = (const float *)a.k + b * a.ks0 + hk * a.ks1;
+  const float *vp = (const float *)a.v + b * a.vs0 + hk * a.vs1;
+  const int row = qb * F32_BM + t;
+
+  float q[D], acc[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    q[d] = row < a.Sq ? qp[row * a.qs2 + d] : 0.0f;
+    acc[d] = 0.0f;
+  }
+  float m = kNegFltMax, lsum = 0.0f;
+  int nkb = (a.Sk + BN - 1) / BN;
+  if (CAUSAL) {
+    int last = qb * F32_BM + F32_BM - 1 + a.off;
+    int lim = last < 0 ? 0 : last / BN + 1;
+    nkb = nkb < lim ? nkb : lim;
+  }
+  for (int jb = 0; jb < nkb; ++jb) {
+    const int key0 = jb * BN;
+    __syncthreads();
+    for (int e = t; e < BN * D; e += 64) {
+      int r = e / D, c = e % D, key = key0 + r;
+      Ks[r][c] = key < a.Sk ? kp[key * a.ks2 + c] : 0.0f;
+      Vs[r][c] = key < a.Sk ? vp[key * a.vs2 + c] : 0.0f;
+    }
+    __syncthreads();
+    float s[BN];
+    float mx = -INFINITY;
+#pragma unroll 4
+    for (int j = 0; j < BN; ++j) {
+      float dot = 0.0f;
+#pragma unroll
+      for (int d = 0; d < D; ++d) dot = fmaf(q[d], Ks[j][d], dot);
+      int key = key0 + j;
+      float sv = dot * a.scale2;
+      if (key >= a.Sk || (CAUSAL && key > row + a.off)) sv = -INFINITY;
+      s[j] = sv;
+      mx = fmaxf(mx, sv);
+    }
+    const float m_new = fmaxf(m, mx);
+    const float alpha = fast_exp2(m - m_new);
+    float rs = 0.0f;
+#pragma unroll
+    for (int j = 0; j < BN; ++j) {
+      s[j] = fast_exp2(s[j] - m_new);
+      rs += s[j];
+    }
+    lsum = lsum * alpha + rs;
+    m = m_new;
+#pragma unroll
+    for (int d = 0; d < D; ++d) acc[d] *= alpha;
+#pragma unroll 4
+    for (int j = 0; j < BN; ++j) {
+      const float p = s[j];
+#pragma unroll
+      for (int d = 0; d < D; ++d) acc[d] = fmaf(p, Vs[j][d], acc[d]);
+    }
+  }
+  if (row < a.Sq) {
+    float *op = (float *)a.o + b * a.os0 + h * a.os1 + row * a.os2;
+#pragma unroll
+    for (int d = 0; d < D; ++d) op[d] = lsum > 0.0f ? acc[d] / lsum : 0.0f;
+    if (a.lse)
+      a.lse[((int64_t)b * a.Hq + h) * a.Sq + row] =
+          lsum > 0.0f ? (m + log2f(lsum)) * kLn2 : -INFINITY;
+  }
+}
+
+template <class E, int D>
+void launch_mfma(const AttnArgs &args, bool causal, int grid, hipStream_t s) {
+  if (causal)
+    hipLaunchKernelGGL((attn_fwd_mfma<E, D, true>), dim3(grid), dim3(NTHR), 0, s, args);
+  else
+    hipLaunchKernelGGL((attn_fwd_mfma<E, D, false>), dim3(grid), dim3(NTHR), 0, s, args);
+}
+
+template <int D>
+void launch_f32(const AttnArgs &args, bool causal, int grid, hipStream_t s) {
+  if (causal)
+    hipLaunchKernelGGL((attn_fwd_f32<D, true>), dim3(grid), dim3(64), 0, s, args);
+  else
+    hipLaunchKernelGGL((attn_fwd_f32<D, false>), dim3(grid), dim3(64), 0, s, args);
+}
+
+}  // namespace
+
+bool attn_supported(const AttnLaunch &a, const char **why) {
+  if (a.dtype == 0) {  // F32
+    if (a.head_dim != 32 && a.head_dim != 64 && a.head_dim != 128) {
+      *why = "fp32 attention supports head_dim 32, 64 or 128";
+      return false;
+    }
+  } else if (a.head_dim != 64 && a.head_dim != 128) {
+    *why = "16-bit attention supports head_dim 64 or 128";
+    return false;
+  }
+  if (a.seq_q > (int64_t)1 << 30 || a.seq_kv > (int64_t)1 << 30 ||
+      a.batch * a.heads_q > (int64_t)1 << 24) {
+    *why = "sequence or batch*heads too large for one launch";
+    return false;
+  }
+  return true;
+}
+
+hipError_t launch_attn_fwd(const AttnLaunch &L, hipStream_t s) {
+  AttnArgs a;
+  a.q = L.q;
+  a.k = L.k;
+  a.v = L.v;
+  a.o = L.o;
+  a.lse = L.lse;
+  a.qs0 = L.qs[0]; a.qs1 = L.qs[1]; a.qs2 = L.qs[2];
+  a.ks0 = L.ks[0]; a.ks1 = L.ks[1]; a.ks2 = L.ks[2];
+  a.vs0 = L.vs[0]; a.vs1 = L.vs[1]; a.vs2 = L.vs[2];
+  a.os0 = L.os[0]; a.os1 = L.os[1]; a.os2 = L.os[2];
+  a.Hq = (int32_t)L.heads_q;
+  a.group = (int32_t)(L.heads_q / L.heads_kv);
+  a.Sq = (int32_t)L.seq_q;
+  a.Sk = (int32_t)L.seq_kv;
+  a.BH = (int32_t)(L.batch * L.heads_q);
+  a.off = (int32_t)(L.seq_kv - L.seq_q);
+  a.scale2 = L.scale_log2;
+  const bool causal = L.causal != 0;
+  if (L.dtype == 0) {
+    a.nqb = (int32_t)((L.seq_q + F32_BM - 1) / F32_BM);
+    int grid = a.nqb * a.BH;
+    switch (L.head_dim) {
+      case 32: launch_f32<32>(a, causal, grid, s); break;
+      case 64: launch_f32<64>(a, causal, grid, s); break;
+      default: launch_f32<128>(a, causal, grid, s); break;
+    }
+  } else {
+    a.nqb = (int32_t)((L.seq_q + BM - 1) / BM);
+    int grid = a.nqb * a.BH;
+    const bool bf16 = L.dtype == 2;
+    if (L.head_dim == 64) {
+      if (bf16) launch_mfma<Bf16Tag, 64>(a, causal, grid, s);
+      else launch_mfma<F16Tag, 64>(a, causal, grid, s);
+    } else {
+      if (bf16) launch_mfma<Bf16Tag, 128>(a, causal, grid, s);
+      else launch_mfma<F16Tag, 128>(a, causal, grid, s);
+    }
+  }
+  return hipGetLastError();
+}
+
+}  // namespace neptune

@@ -1,0 +1,61 @@
+// kernels.h — host-side launch interface between the C-ABI layer (abi.cpp)
+// and the HIP kernels. Arguments are already validated and resolved.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace neptune {
+
+struct AttnLaunch {
+  const void *q, *k, *v;
+  void *o;
+  float *lse;  // nullable
+  int64_t batch, heads_q, heads_kv, seq_q, seq_kv, head_dim;
+  int64_t qs[3], ks[3], vs[3], os[3];  // (batch, head, seq) strides, elements
+  int32_t dtype;
+  int32_t causal;
+  float scale_log2;
+};
+
+struct DecodeLaunch {
+  const void *q, *k, *v;
+  const float *k_scale, *v_scale;  // fp8 only
+  void *o;
+  float *lse;        // nullable
+  float *part_o;     // [batch, heads_q, splits, head_dim]
+  float *part_ml;    // [batch, heads_q, splits, 2]
+  int64_t batch, heads_q, heads_kv, seq_kv, head_dim;
+  int64_t splits, chunk, scale_block, n_scale_blocks;
+  int32_t kv_dtype;
+  float scale_log2;
+};
+
+struct QuantLaunch {
+  const void *src;
+  uint8_t *codes;
+  float *scales;
+  int64_t batch, heads_kv, seq_kv, head_dim, scale_block, n_scale_blocks;
+};
+
+struct ScanLaunch {
+  const void *u, *delta_raw, *B, *C, *z;
+  const float *A, *D, *delta_bias;
+  void *y;
+  int64_t batch, dim, seq_len, d_state;
+  int32_t delta_softplus;
+};
+
+// Each returns hipSuccess or the launch error. Shapes the kernels do not
+// cover are rejected by the ABI layer before these are called.
+hipError_t launch_attn_fwd(const AttnLaunch &a, hipStream_t s);
+hipError_t launch_decode(const DecodeLaunch &a, hipStream_t s);
+hipError_t launch_kv_quantize(const QuantLaunch &a, hipStream_t s);
+hipError_t launch_selective_scan(const ScanLaunch &a, hipStream_t s);
+
+// Coverage predicates used by the ABI layer for NEPTUNE_ERR_UNSUPPORTED.
+bool attn_supported(const AttnLaunch &a, const char **why);
+bool decode_supported(const DecodeLaunch &a, const char **why);
+bool scan_supported(const ScanLaunch &a, const char **why);
+
+}  // namespace neptune

@@ -1,0 +1,51 @@
+"""Shared test utilities: seeded inputs, storage-bit views and tolerances."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+import oracle
+
+# Tolerances from the north-star contract, written here once.
+TOL_F32_REL = 1e-5      # fp32: max|a-b| <= 1e-5 * max|ref|
+TOL_BF16_ABS = 2e-2     # bf16: max-abs
+TOL_FP8_ABS = 6e-2      # fp8 KV: max-abs
+TOL_LSE_ABS = 1e-3      # logsumexp (fp32 output)
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    """Storage bits of a CPU/GPU tensor as the numpy type the oracle takes."""
+    t = t.detach().to("cpu").contiguous()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    if t.dtype == torch.float16:
+        return t.numpy()
+    if t.dtype == torch.float32:
+        return t.numpy()
+    if t.dtype == torch.uint8:
+        return t.numpy()
+    raise TypeError(t.dtype)
+
+
+def from_bf16_bits(b: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(b).view(np.int16)).view(torch.bfloat16)
+
+
+def to_f32(t: torch.Tensor) -> np.ndarray:
+    return t.detach().to("cpu").float().numpy()
+
+
+def oracle_dtype(t: torch.Tensor) -> int:
+    return {torch.float32: oracle.F32, torch.float16: oracle.F16,
+            torch.bfloat16: oracle.BF16}[t.dtype]
+
+
+def randn(shape, seed: int, dtype=torch.bfloat16, scale: float = 1.0, device="cpu"):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    x = torch.randn(shape, generator=g, dtype=torch.float32) * scale
+    return x.to(dtype).to(device)
+
+
+def max_abs(a: np.ndarray, b: np.ndarray) -> float:
+    return float(np.max(np.abs(a.astype(np.float64) - b.astype(np.float64)))) if a.size else 0.0
