@@ -1,0 +1,302 @@
+"""CPU tests of the drop-in boundary (include/neptune_hip.h).
+
+No kernel runs here: every check is one the library answers on the host
+before any HIP call (symbol export, descriptor layout, the backend info
+record, argument validation and its status codes, the no-device path).
+The classes of failure mirror the reference's: invalid input and
+unsupported requests (NotImplementedError, translators/common.py:187-197),
+runtime failures (RuntimeError, common.py:217-224).
+"""
+
+import ctypes
+import re
+import subprocess
+import threading
+from pathlib import Path
+
+import pytest
+
+import oracle
+from neptune_hip import _abi
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "neptune_hip.h"
+
+# Plausible-looking, 16-byte aligned device addresses. They are only ever
+# passed to calls that must fail validation (or find no device) before any
+# HIP work is enqueued; test_no_device_path runs only where no device exists.
+FAKE = 0x10000
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _abi.load_library()
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"NEPTUNE_API[^;{]*?\b(neptune_\w+)\s*\(", text, re.S)))
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_symbols()
+    assert len(names) >= 8
+    assert sorted(_abi.EXPORTED_SYMBOLS) == names
+    so = _abi.find_library_path()
+    out = subprocess.run(["nm", "-D", "--defined-only", str(so)], check=True,
+                         capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (neptune_\w+)$", out, re.M))
+    assert set(names) <= exported
+    for n in names:
+        assert hasattr(lib, n)
+
+
+def test_library_does_not_link_the_oracle():
+    so = _abi.find_library_path()
+    out = subprocess.run(["nm", "-D", str(so)], check=True, capture_output=True,
+                         text=True).stdout
+    assert "neptune_cpu_" not in out
+    deps = subprocess.run(["ldd", str(so)], capture_output=True, text=True).stdout
+    assert "oracle" not in deps
+
+
+def test_backend_info(lib):
+    info = _abi.backend_info(lib)
+    assert info["abi_version"] == _abi.ABI_VERSION == 1
+    assert info["name"] == "NeptuneHTileHIP"
+    assert info["gcn_arch"] == "gfx950"
+    assert isinstance(info["hip_runtime_version"], int)
+    assert lib.neptune_hip_get_backend_info(None) == _abi.ERR_INVALID_ARGUMENT
+    assert b"NULL" in lib.neptune_last_error()
+
+
+_LAYOUT_C = r"""
+#include <stddef.h>
+#include <stdio.h>
+#include "neptune_hip.h"
+#define F(T, f) printf(#T " " #f " %zu\n", offsetof(T, f));
+#define S(T) printf(#T " sizeof %zu\n", sizeof(T));
+int main(void) {
+  F(neptune_attn_desc, batch) F(neptune_attn_desc, heads_q) F(neptune_attn_desc, heads_kv)
+  F(neptune_attn_desc, seq_q) F(neptune_attn_desc, seq_kv) F(neptune_attn_desc, head_dim)
+  F(neptune_attn_desc, q_stride) F(neptune_attn_desc, k_stride) F(neptune_attn_desc, v_stride)
+  F(neptune_attn_desc, o_stride) F(neptune_attn_desc, dtype) F(neptune_attn_desc, causal)
+  F(neptune_attn_desc, scale_log2) F(neptune_attn_desc, reserved) S(neptune_attn_desc)
+  F(neptune_decode_desc, batch) F(neptune_decode_desc, heads_q) F(neptune_decode_desc, heads_kv)
+  F(neptune_decode_desc, seq_kv) F(neptune_decode_desc, head_dim)
+  F(neptune_decode_desc, num_splits) F(neptune_decode_desc, scale_block)
+  F(neptune_decode_desc, q_dtype) F(neptune_decode_desc, kv_dtype)
+  F(neptune_decode_desc, scale_log2) F(neptune_decode_desc, reserved) S(neptune_decode_desc)
+  F(neptune_scan_desc, batch) F(neptune_scan_desc, dim) F(neptune_scan_desc, seq_len)
+  F(neptune_scan_desc, d_state) F(neptune_scan_desc, io_dtype)
+  F(neptune_scan_desc, delta_softplus) S(neptune_scan_desc)
+  F(neptune_backend_info, abi_version) F(neptune_backend_info, name)
+  F(neptune_backend_info, gcn_arch) F(neptune_backend_info, hip_runtime_version)
+  S(neptune_backend_info)
+  return 0;
+}
+"""
+
+
+def test_ctypes_descriptors_match_the_c_header(tmp_path):
+    """Offsets and sizes the C compiler gives the header's structs equal
+    the ctypes declarations of both the product package and the oracle."""
+    src = tmp_path / "layout.c"
+    src.write_text(_LAYOUT_C)
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-I", str(ROOT / "include"), str(src), "-o", str(exe)],
+                   check=True)
+    c = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True,
+                               text=True).stdout.splitlines():
+        t, f, n = line.split()
+        c[(t, f)] = int(n)
+    pairs = [("neptune_attn_desc", _abi.AttnDesc, oracle.AttnDesc),
+             ("neptune_decode_desc", _abi.DecodeDesc, oracle.DecodeDesc),
+             ("neptune_scan_desc", _abi.ScanDesc, oracle.ScanDesc),
+             ("neptune_backend_info", _abi.BackendInfo, None)]
+    for cname, prod, orc in pairs:
+        for cls in (prod, orc):
+            if cls is None:
+                continue
+            assert ctypes.sizeof(cls) == c[(cname, "sizeof")], (cname, cls)
+            for fname, _ in cls._fields_:
+                assert getattr(cls, fname).offset == c[(cname, fname)], (cname, fname)
+
+
+def _attn_desc(**kw):
+    d = _abi.AttnDesc()
+    d.batch, d.heads_q, d.heads_kv, d.seq_q, d.seq_kv, d.head_dim = 1, 4, 2, 256, 256, 128
+    d.dtype = _abi.DTYPE_BF16
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+def _attn(lib, d, ptrs=(FAKE, FAKE, FAKE, FAKE)):
+    return lib.neptune_attn_fwd(ctypes.byref(d) if d is not None else None, *ptrs, None, None)
+
+
+@pytest.mark.parametrize("field,value,status", [
+    ("batch", 0, _abi.ERR_INVALID_ARGUMENT),
+    ("seq_q", -1, _abi.ERR_INVALID_ARGUMENT),
+    ("head_dim", 0, _abi.ERR_INVALID_ARGUMENT),
+    ("heads_kv", 3, _abi.ERR_INVALID_ARGUMENT),         # 4 % 3 != 0
+    ("dtype", _abi.DTYPE_FP8_E4M3, _abi.ERR_UNSUPPORTED),
+    ("dtype", 17, _abi.ERR_UNSUPPORTED),
+    ("head_dim", 96, _abi.ERR_UNSUPPORTED),
+    ("scale_log2", float("nan"), _abi.ERR_INVALID_ARGUMENT),
+    ("scale_log2", -1.0, _abi.ERR_INVALID_ARGUMENT),
+])
+def test_attn_validation(lib, field, value, status):
+    assert _attn(lib, _attn_desc(**{field: value})) == status
+    assert lib.neptune_last_error()
+
+
+def test_attn_null_and_stride_errors(lib):
+    assert _attn(lib, None) == _abi.ERR_INVALID_ARGUMENT
+    assert _attn(lib, _attn_desc(), (FAKE, 0, FAKE, FAKE)) == _abi.ERR_INVALID_ARGUMENT
+    d = _attn_desc()
+    d.q_stride[:] = (0, 128, 1)  # mixed zero / positive
+    assert _attn(lib, d) == _abi.ERR_INVALID_ARGUMENT
+    d = _attn_desc()
+    d.k_stride[:] = (256 * 128 * 2, 256 * 128, 132)  # not a multiple of 8 elements
+    assert _attn(lib, d) == _abi.ERR_UNSUPPORTED
+    assert _attn(lib, _attn_desc(), (FAKE + 2, FAKE, FAKE, FAKE)) == _abi.ERR_UNSUPPORTED
+    assert b"aligned" in lib.neptune_last_error()
+
+
+def _dec_desc(**kw):
+    d = _abi.DecodeDesc()
+    d.batch, d.heads_q, d.heads_kv, d.seq_kv, d.head_dim = 2, 8, 2, 1000, 128
+    d.num_splits, d.scale_block = 3, 64
+    d.q_dtype, d.kv_dtype = _abi.DTYPE_BF16, _abi.DTYPE_BF16
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+def test_decode_workspace_matches_layout(lib):
+    d = _dec_desc()
+    n = ctypes.c_size_t()
+    assert lib.neptune_decode_workspace_bytes(ctypes.byref(d), ctypes.byref(n)) == _abi.OK
+    splits, _ = oracle.decode_layout(2, 2, 1000, 3)
+    rows = 2 * 8 * splits
+    align = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    assert n.value == align(rows * 128 * 4) + align(rows * 2 * 4)
+    assert lib.neptune_decode_workspace_bytes(ctypes.byref(d), None) == _abi.ERR_INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("B,Hk,L,splits", [(16, 8, 32768, 16), (2, 2, 1000, 3), (1, 1, 100000, 0),
+                                           (4, 2, 50, 0), (3, 1, 4097, 0), (1, 1, 64, 7)])
+def test_decode_split_rule_agrees_with_oracle(lib, B, Hk, L, splits):
+    """The library's workspace size follows the split count the oracle
+    computes for the same request."""
+    d = _dec_desc(batch=B, heads_q=Hk, heads_kv=Hk, seq_kv=L, num_splits=splits)
+    n = ctypes.c_size_t()
+    assert lib.neptune_decode_workspace_bytes(ctypes.byref(d), ctypes.byref(n)) == _abi.OK
+    s, c = oracle.decode_layout(B, Hk, L, splits)
+    assert c % 64 == 0 and (s - 1) * c < L <= s * c
+    rows = B * Hk * s
+    assert n.value == (rows * 128 * 4 + 255) // 256 * 256 + (rows * 8 + 255) // 256 * 256
+
+
+def _decode(lib, d, ws_bytes=1 << 30, kscale=None, ptrs=(FAKE, FAKE, FAKE)):
+    return lib.neptune_decode_splitk(ctypes.byref(d), *ptrs, kscale, kscale, FAKE, None, FAKE,
+                                     ws_bytes, None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    ({"heads_q": 5}, _abi.ERR_INVALID_ARGUMENT),           # 5 % 2
+    ({"seq_kv": 0}, _abi.ERR_INVALID_ARGUMENT),
+    ({"num_splits": -1}, _abi.ERR_INVALID_ARGUMENT),
+    ({"q_dtype": _abi.DTYPE_F16}, _abi.ERR_UNSUPPORTED),
+    ({"kv_dtype": _abi.DTYPE_F32}, _abi.ERR_UNSUPPORTED),
+    ({"head_dim": 64}, _abi.ERR_UNSUPPORTED),
+    ({"heads_q": 64, "heads_kv": 2}, _abi.ERR_UNSUPPORTED),  # group 32 > 16
+])
+def test_decode_validation(lib, kw, status):
+    assert _decode(lib, _dec_desc(**kw)) == status
+    assert lib.neptune_last_error()
+
+
+def test_decode_workspace_and_fp8_errors(lib):
+    assert _decode(lib, _dec_desc(), ws_bytes=16) == _abi.ERR_WORKSPACE_TOO_SMALL
+    assert b"need" in lib.neptune_last_error()
+    fp8 = _dec_desc(kv_dtype=_abi.DTYPE_FP8_E4M3)
+    assert _decode(lib, fp8) == _abi.ERR_INVALID_ARGUMENT            # scales missing
+    assert _decode(lib, _dec_desc(kv_dtype=_abi.DTYPE_FP8_E4M3, scale_block=48),
+                   kscale=FAKE) == _abi.ERR_UNSUPPORTED              # not a multiple of 32
+    assert _decode(lib, _dec_desc(), ptrs=(FAKE, FAKE, 0)) == _abi.ERR_INVALID_ARGUMENT
+
+
+def test_quantize_and_scan_validation(lib):
+    q = lib.neptune_kv_quantize_fp8
+    assert q(1, 1, 64, 128, 64, None, FAKE, FAKE, None) == _abi.ERR_INVALID_ARGUMENT
+    assert q(1, 0, 64, 128, 64, FAKE, FAKE, FAKE, None) == _abi.ERR_INVALID_ARGUMENT
+    d = _abi.ScanDesc(1, 64, 128, 16, _abi.DTYPE_BF16, 1)
+    s = lib.neptune_selective_scan_fwd
+    assert s(None, *([FAKE] * 9), None) == _abi.ERR_INVALID_ARGUMENT
+    bad = _abi.ScanDesc(1, 64, 0, 16, _abi.DTYPE_BF16, 1)
+    assert s(ctypes.byref(bad), *([FAKE] * 9), None) == _abi.ERR_INVALID_ARGUMENT
+    f16 = _abi.ScanDesc(1, 64, 128, 16, _abi.DTYPE_F16, 1)
+    assert s(ctypes.byref(f16), *([FAKE] * 9), None) == _abi.ERR_UNSUPPORTED
+    n8 = _abi.ScanDesc(1, 64, 128, 8, _abi.DTYPE_BF16, 1)
+    assert s(ctypes.byref(n8), *([FAKE] * 9), None) == _abi.ERR_UNSUPPORTED
+    assert s(ctypes.byref(d), FAKE, FAKE, FAKE, FAKE, None, FAKE, FAKE, FAKE, FAKE,
+             None) == _abi.ERR_INVALID_ARGUMENT  # C missing
+
+
+def test_no_device_path(lib):
+    """A fully valid request on a host without a HIP device reports
+    NO_DEVICE instead of crashing (never reached where a device exists)."""
+    if lib.neptune_device_count() > 0:
+        pytest.skip("a HIP device is visible; the no-device path is not reachable")
+    assert _attn(lib, _attn_desc()) == _abi.ERR_NO_DEVICE
+    assert b"no HIP device" in lib.neptune_last_error()
+    with pytest.raises(_abi.NeptuneNoDevice):
+        _abi.check(_abi.ERR_NO_DEVICE, lib)
+
+
+def test_error_text_is_thread_local(lib):
+    assert _attn(lib, _attn_desc(batch=0)) == _abi.ERR_INVALID_ARGUMENT
+    mine = lib.neptune_last_error()
+    other = {}
+
+    def worker():
+        other["before"] = lib.neptune_last_error()
+        _abi.backend_info(lib)
+        other["after"] = lib.neptune_last_error()
+
+    t = threading.Thread(target=worker)
+    t.start()
+    t.join()
+    assert other["before"] == b"" and other["after"] == b""
+    assert lib.neptune_last_error() == mine
+
+
+def test_status_to_exception_mapping(lib):
+    assert _attn(lib, _attn_desc(head_dim=96)) == _abi.ERR_UNSUPPORTED
+    with pytest.raises(NotImplementedError):
+        _abi.check(_abi.ERR_UNSUPPORTED, lib)
+    with pytest.raises(ValueError):
+        _abi.check(_abi.ERR_INVALID_ARGUMENT, lib)
+    with pytest.raises(_abi.NeptuneWorkspaceTooSmall):
+        _abi.check(_abi.ERR_WORKSPACE_TOO_SMALL, lib)
+    with pytest.raises(RuntimeError):
+        _abi.check(_abi.ERR_HIP, lib)
+
+
+def test_locator_order(tmp_path, monkeypatch):
+    """Explicit path, then NEPTUNE_HIP_LIB, then the package's _native dir
+    (the reference's plugin resolution order, src/neptune_mlir/plugin.py:28-55)."""
+    fake = tmp_path / "libneptune_hip.so"
+    fake.write_bytes(b"")
+    monkeypatch.delenv(_abi.DEFAULT_LIBRARY_ENV, raising=False)
+    default = _abi.find_library_path()
+    assert default is not None and default.parent.name == "_native"
+    assert _abi.find_library_path(fake) == fake.resolve()
+    monkeypatch.setenv(_abi.DEFAULT_LIBRARY_ENV, str(fake))
+    assert _abi.find_library_path() == fake.resolve()
+    monkeypatch.setenv(_abi.DEFAULT_LIBRARY_ENV, str(tmp_path / "missing.so"))
+    assert _abi.find_library_path() == default
