@@ -156,6 +156,44 @@ def cpu_baseline_prefill(res, budget_s=15.0, max_heads=32):
     }
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.txt"
+
+
+def measured_traffic():
+    """HBM bytes per launch per workload, from the rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes summarised in profiles/hbm_traffic.txt (lines
+    'workload bytes'); {} when that summary is absent."""
+    out = {}
+    if TRAFFIC_FILE.is_file():
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            parts = line.split("#", 1)[0].split()
+            if len(parts) == 2:
+                out[parts[0]] = float(parts[1])
+    return out
+
+
+def bench_copy(torch, steps, warmup, nbytes=1 << 30):
+    """A plain device-to-device copy of known size: the calibration kernel
+    for the HBM byte counters."""
+    src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    wall, ev = time_launches(lambda _: dst.copy_(src), steps, warmup)
+    return "copy 1 GiB", wall, ev, 2 * nbytes
+
+
+def hbm_entry(key, name, wall, ev, nbytes, steps, traffic):
+    gbs = nbytes / ev / 1e9
+    return {
+        "workload": name,
+        "value": round(nbytes * steps / wall / 1e9, 1),
+        "unit": "GB/s",
+        "us_per_step": round(ev * 1e6, 2),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "traffic": traffic.get(key)},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -163,13 +201,18 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the decode/scan configurations")
+    ap.add_argument("--workload", default="all",
+                    choices=["all", "prefill", "decode", "decode_fp8", "scan", "copy"],
+                    help="run one configuration only (for profiling); 'copy' is a plain "
+                         "1 GiB device copy used to calibrate HBM byte counters")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(json.dumps({"error": "this backend runs on one GPU; multi-GPU sharding is a "
-                          "design note only (no collectives are built)", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this backend runs on one GPU only: the multi-GPU "
+                          "sharding of this path is a design note, no collectives are built",
+                          "n_gpus": args.gpus}))
         sys.exit(2)
 
     import torch
@@ -179,6 +222,19 @@ def main():
     torch.cuda.set_device(0)
     arch = torch.cuda.get_device_properties(0).gcnArchName
     print(f"# device {torch.cuda.get_device_name(0)} {arch}", file=sys.stderr, flush=True)
+    traffic = measured_traffic()
+
+    single = {
+        "decode": lambda: bench_decode(ops, torch, args.steps, args.warmup, fp8=False),
+        "decode_fp8": lambda: bench_decode(ops, torch, args.steps, args.warmup, fp8=True),
+        "scan": lambda: bench_scan(ops, torch, args.steps, args.warmup),
+        "copy": lambda: bench_copy(torch, args.steps, args.warmup),
+    }
+    if args.workload in single:
+        name, wall, ev, nbytes = single[args.workload]()
+        print(json.dumps(hbm_entry(args.workload, name, wall, ev, nbytes, args.steps, traffic)),
+              flush=True)
+        return
 
     res = bench_prefill(ops, torch, args.steps, args.warmup)
     value = res["flops"] * args.steps / res["wall"] / 1e12
@@ -187,27 +243,20 @@ def main():
           file=sys.stderr, flush=True)
 
     secondary = []
-    if not args.no_secondary:
+    if not args.no_secondary and args.workload == "all":
         del res["k"], res["v"]
         torch.cuda.empty_cache()
         sec_steps, sec_warm = min(args.steps, 20), min(args.warmup, 3)
-        for fn in (lambda: bench_decode(ops, torch, sec_steps, sec_warm, fp8=False),
-                   lambda: bench_decode(ops, torch, sec_steps, sec_warm, fp8=True),
-                   lambda: bench_scan(ops, torch, sec_steps, sec_warm)):
+        for key, fn in (("decode", lambda: bench_decode(ops, torch, sec_steps, sec_warm, False)),
+                        ("decode_fp8", lambda: bench_decode(ops, torch, sec_steps, sec_warm,
+                                                            True)),
+                        ("scan", lambda: bench_scan(ops, torch, sec_steps, sec_warm))):
             name, wall, ev, nbytes = fn()
-            gbs = nbytes / ev / 1e9
-            secondary.append({
-                "workload": name,
-                "value": round(nbytes * sec_steps / wall / 1e9, 1),
-                "unit": "GB/s",
-                "us_per_step": round(ev * 1e6, 2),
-                "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                             "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                             "traffic": None},
-            })
-            print(f"# {name}: {ev * 1e6:.1f} us, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
+            secondary.append(hbm_entry(key, name, wall, ev, nbytes, sec_steps, traffic))
+            print(f"# {name}: {ev * 1e6:.1f} us, {nbytes / ev / 1e9:.0f} GB/s", file=sys.stderr,
+                  flush=True)
             torch.cuda.empty_cache()
-        # the prefill inputs are still needed for the CPU sample
+        # the prefill inputs are needed again for the CPU sample
         g = torch.Generator(device="cuda").manual_seed(2)
         shape = res["q"].shape
         res["q"], res["k"], res["v"] = (
@@ -235,7 +284,8 @@ def main():
                    "causal": True, "flops_per_step": res["flops"]},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": traffic.get("prefill")},
         "cpu_baseline": cpu,
         "secondary": secondary,
     }
