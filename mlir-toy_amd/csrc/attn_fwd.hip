@@ -25,6 +25,7 @@
 // tile is consumed, and one barrier per key block separates the phases.
 #include "device_common.h"
 #include "kernels.h"
+#include "attn_args.h"
 
 namespace neptune {
 namespace {
@@ -33,14 +34,6 @@ constexpr int BM = 128;  // query rows per work-group (HTile %c128)
 constexpr int BN = 64;   // keys per block (HTile %c64)
 constexpr int NTHR = 256;
 
-struct AttnArgs {
-  const void *q, *k, *v;
-  void *o;
-  float *lse;
-  int64_t qs0, qs1, qs2, ks0, ks1, ks2, vs0, vs1, vs2, os0, os1, os2;
-  int32_t Hq, group, Sq, Sk, nqb, BH, off;  // off = Sk - Sq (causal diagonal)
-  float scale2;                             // log2(e)/sqrt(D) unless given
-};
 
 __device__ inline uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
   return __builtin_amdgcn_perm(hi, lo, sel);
@@ -403,8 +396,7 @@ hipError_t launch_attn_fwd(const AttnLaunch &L, hipStream_t s) {
       if (bf16) launch_mfma<Bf16Tag, 64>(a, causal, grid, s);
       else launch_mfma<F16Tag, 64>(a, causal, grid, s);
     } else {
-      if (bf16) launch_mfma<Bf16Tag, 128>(a, causal, grid, s);
-      else launch_mfma<F16Tag, 128>(a, causal, grid, s);
+      return launch_attn_d128(a, L.dtype, causal, s);
     }
   }
   return hipGetLastError();
