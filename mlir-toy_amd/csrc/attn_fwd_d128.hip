@@ -40,6 +40,7 @@ constexpr int BN = 64;
 constexpr int HD = 128;
 constexpr int NT = 256;
 constexpr int TILE = BN * HD * 2;  // bytes per K or V tile (16 KiB)
+constexpr float kSlack = 8.0f;     // lazy-rescale threshold (log2 units)
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
@@ -188,9 +189,23 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
       mx = pair_max(mx);
-      const float m_new = fmaxf(m, mx * sc);
-      const float alpha = fast_exp2(m - m_new);
-      const float nm = -m_new;
+      // Lazy rescaling: the running max m only moves when a row's block max
+      // exceeds it by more than kSlack (a factor 2^kSlack); in between,
+      // p = 2^(s - m) <= 2^kSlack, which the fp32 sums hold exactly as well
+      // and whose 16-bit rounding is relative, so results differ from a
+      // rescale at every block by rounding only.
+      const float m_blk = mx * sc;
+      if (__any(m_blk > m + kSlack)) {
+        const float m_new = fmaxf(m, m_blk);
+        const float alpha = fast_exp2(m - m_new);
+        lsum *= alpha;
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[nb][r] *= alpha;
+        m = m_new;
+      }
+      const float nm = -m;
       float rs = 0.0f;
       u32x4 pf[4];
 #pragma unroll
@@ -205,12 +220,7 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a) {
           pf[c][i] = E::pack2(p0, p1);
         }
       }
-      lsum = lsum * alpha + rs;
-      m = m_new;
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[nb][r] *= alpha;
+      lsum += rs;
 
       // O^T += V^T P^T for this block (A operand by transpose reads)
       const uint8_t *vt = vt0 + (jb & 1) * TILE;

@@ -15,6 +15,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -32,8 +34,9 @@ struct Bf16Tag {
     __bf16 b = (__bf16)f;
     return __builtin_bit_cast(uint16_t, b);
   }
+  // two values, round to nearest even, in one v_cvt_pk_bf16_f32
   __device__ static inline uint32_t pack2(float lo, float hi) {
-    return uint32_t(from_f32(lo)) | (uint32_t(from_f32(hi)) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
   }
   __device__ static inline f32x16 mfma32(vec8 a, vec8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -52,8 +55,9 @@ struct F16Tag {
     _Float16 h = (_Float16)f;
     return __builtin_bit_cast(uint16_t, h);
   }
+  // two values, round to nearest even, in one v_cvt_pk_f16_f32
   __device__ static inline uint32_t pack2(float lo, float hi) {
-    return uint32_t(from_f32(lo)) | (uint32_t(from_f32(hi)) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, f16x2));
   }
   __device__ static inline f32x16 mfma32(vec8 a, vec8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
