@@ -24,10 +24,11 @@
 //   K: unit u of row r at u ^ (r & 15)   (reads: 32 rows, one unit each)
 //   V: unit u of row r at u ^ 4(r & 3)   (transpose reads: 4 rows x 64 B)
 //
-// Work-group order: with batch*heads a multiple of 8, work-group id % 8 is
-// the XCD it is dispatched to; each XCD walks its own heads one at a time,
-// causal query blocks heaviest first, so the K/V of the heads in flight on
-// an XCD stay in that XCD's L2.
+// Work-groups: each runs two query blocks of one head, q0 = nqb-1-p and
+// q1 = p, back to back; the K/V stream simply continues from q0's last key
+// block into q1's first, so q1's tiles (and its Q^T) load while q0 drains.
+// Under the causal mask the pair's key-block count is the same for every p,
+// so all work-groups carry equal work (no tail of heavy stragglers).
 #include "attn_args.h"
 #include "device_common.h"
 #include "kernels.h"
@@ -49,20 +50,53 @@ typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 __device__ inline lds_void *as_lds(const uint8_t *p) { return (lds_void *)(p); }
 
 // Wave w copies rows [16w, 16w+16) of a 64 x 128 tile (four 1 KiB chunks of
-// four rows) straight into LDS. Rows past the end of the sequence re-read
-// the last row: their scores are masked, so their P is exactly 0.
+// four rows) straight into LDS. Full blocks take a wave-uniform base pointer
+// plus per-lane 32-bit offsets fixed for the whole kernel, so issuing a
+// chunk costs no vector ALU work; a block that runs past the end of the
+// sequence re-reads the last row instead (its scores are masked, so its P
+// is exactly 0).
+struct TileLoader {
+  const char *base;   // element (0, 0) of this (batch, head)
+  int64_t row_bytes;  // key stride in bytes
+  uint32_t off[4];    // per-lane byte offset of chunk c within a full block
+  int lane_row;       // 16 w + lane / 16: row of chunk 0 for this lane
+  int sw_base;        // lane & 15
+};
+
 template <bool IS_V>
-__device__ inline void tile_to_lds(const uint16_t *src, int64_t stride, int key0, int Sk,
-                                   const uint8_t *tile, int w, int lane) {
+__device__ inline TileLoader make_loader(const uint16_t *src, int64_t stride, int w, int lane) {
+  TileLoader t;
+  t.base = (const char *)src;
+  t.row_bytes = stride * 2;
+  t.lane_row = 16 * w + (lane >> 4);
+  t.sw_base = lane & 15;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    const int q = 4 * w + c;
-    const int r = 4 * q + (lane >> 4);
-    const int sw = IS_V ? ((r & 3) << 2) : (r & 15);
-    const int unit = (lane & 15) ^ sw;
-    const int key = min(key0 + r, Sk - 1);
-    __builtin_amdgcn_global_load_lds(src + (int64_t)key * stride + unit * 8,
-                                     as_lds(tile + q * 1024), 16, 0, 0);
+    const int r = t.lane_row + 4 * c;
+    const int unit = (lane & 15) ^ (IS_V ? ((r & 3) << 2) : (r & 15));
+    t.off[c] = (uint32_t)((int64_t)r * t.row_bytes + unit * 16);
+  }
+  return t;
+}
+
+template <bool IS_V>
+__device__ inline void tile_to_lds(const TileLoader &t, int key0, int Sk, const uint8_t *tile,
+                                   int w) {
+  if (key0 + BN <= Sk) {
+    const char *blk = t.base + (int64_t)key0 * t.row_bytes;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      __builtin_amdgcn_global_load_lds(blk + t.off[c], as_lds(tile + (4 * w + c) * 1024), 16, 0,
+                                       0);
+  } else {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int r = t.lane_row + 4 * c;
+      const int unit = t.sw_base ^ (IS_V ? ((r & 3) << 2) : (r & 15));
+      const int key = min(key0 + r, Sk - 1);
+      __builtin_amdgcn_global_load_lds(t.base + (int64_t)key * t.row_bytes + unit * 16,
+                                       as_lds(tile + (4 * w + c) * 1024), 16, 0, 0);
+    }
   }
 }
 
@@ -78,20 +112,27 @@ __device__ inline float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-__device__ inline void map_block(const AttnArgs &a, int id, bool causal, int *qb, int *bh) {
+// Work-group -> (batch*head, pair of query blocks). A work-group runs query
+// blocks q0 = nqb-1-p and q1 = p of one head; under the causal mask their
+// key-block counts add up to the same total for every p, so all work-groups
+// carry equal work and the grid has no tail of heavy stragglers. With
+// batch*heads a multiple of 8, work-group id % 8 is the XCD it is dispatched
+// to and each XCD walks its own heads in order, so the K/V of the heads in
+// flight on an XCD stay in that XCD's L2.
+__device__ inline void map_block(const AttnArgs &a, int npair, int id, int *pair, int *bh) {
   if ((a.BH & 7) == 0) {
     const int x = id & 7, k = id >> 3;
-    const int t = k / a.nqb, r = k - t * a.nqb;
+    const int t = k / npair;
     *bh = x + 8 * t;
-    *qb = causal ? a.nqb - 1 - r : r;
+    *pair = k - t * npair;
   } else {
     *bh = id % a.BH;
-    *qb = causal ? a.nqb - 1 - id / a.BH : id / a.BH;
+    *pair = id / a.BH;
   }
 }
 
 template <class E, bool CAUSAL>
-__global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a) {
+__global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a, int npair) {
   typedef typename E::vec8 V8;
   __shared__ __attribute__((aligned(16))) uint8_t smem[4 * TILE];  // K0 K1 V0 V1
   const uint8_t *const kt0 = smem;
@@ -102,37 +143,52 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane & 31, g = lane >> 5;
 
-  int qb, bh;
-  map_block(a, blockIdx.x, CAUSAL, &qb, &bh);
+  int pair, bh;
+  map_block(a, npair, blockIdx.x, &pair, &bh);
   const int b = bh / a.Hq, h = bh - b * a.Hq, hk = h / a.group;
   const uint16_t *qp = (const uint16_t *)a.q + b * a.qs0 + h * a.qs1;
   const uint16_t *kp = (const uint16_t *)a.k + b * a.ks0 + hk * a.ks1;
   const uint16_t *vp = (const uint16_t *)a.v + b * a.vs0 + hk * a.vs1;
 
-  const int row0 = qb * BM + w * 32;
-  const int row = row0 + lq;
-
-  int nkb = (a.Sk + BN - 1) / BN;  // key blocks of the work-group
-  int nkw = nkb;                    // key blocks this wave computes
-  if (CAUSAL) {
-    const int last_wg = qb * BM + BM - 1 + a.off;
-    nkb = min(nkb, last_wg < 0 ? 0 : last_wg / BN + 1);
-    const int last_w = row0 + 31 + a.off;
-    nkw = min(nkb, last_w < 0 ? 0 : last_w / BN + 1);
-  }
-
-  if (nkb > 0) {
-    tile_to_lds<false>(kp, a.ks2, 0, a.Sk, kt0, w, lane);
-    tile_to_lds<true>(vp, a.vs2, 0, a.Sk, vt0, w, lane);
-    if (nkb > 1) tile_to_lds<false>(kp, a.ks2, BN, a.Sk, kt0 + TILE, w, lane);
-  }
-
-  // Q^T operand: k-step st covers head_dim 16 st + 8 g .. +7 of this row
-  u32x4 qf[8];
+  // the two query blocks (the heavier first); a lone middle block has n1 = 0
+  const int qbs[2] = {a.nqb - 1 - pair, pair};
+  const bool two = qbs[1] != qbs[0];
+  int nkb[2], nkw[2];  // key blocks per query block: work-group, this wave
 #pragma unroll
-  for (int st = 0; st < 8; ++st)
-    qf[st] = row < a.Sq ? *(const u32x4 *)(qp + row * a.qs2 + 16 * st + 8 * g)
-                        : u32x4{0, 0, 0, 0};
+  for (int it = 0; it < 2; ++it) {
+    int n = (a.Sk + BN - 1) / BN, nw = n;
+    if (CAUSAL) {
+      const int last_wg = qbs[it] * BM + BM - 1 + a.off;
+      n = min(n, last_wg < 0 ? 0 : last_wg / BN + 1);
+      const int last_w = qbs[it] * BM + w * 32 + 31 + a.off;
+      nw = min(n, last_w < 0 ? 0 : last_w / BN + 1);
+    }
+    nkb[it] = (it == 1 && !two) ? 0 : n;
+    nkw[it] = (it == 1 && !two) ? 0 : nw;
+  }
+  const int n0 = nkb[0];
+  const int nv = n0 + nkb[1];  // virtual key blocks: n0 for q0, then q1's
+
+  const TileLoader kl = make_loader<false>(kp, a.ks2, w, lane);
+  const TileLoader vl = make_loader<true>(vp, a.vs2, w, lane);
+  // virtual block t -> key block of its query block; K/V slot t & 1
+  auto vkey0 = [&](int t) { return (t < n0 ? t : t - n0) * BN; };
+  if (nv > 0) {
+    tile_to_lds<false>(kl, vkey0(0), a.Sk, kt0, w);
+    tile_to_lds<true>(vl, vkey0(0), a.Sk, vt0, w);
+    if (nv > 1) tile_to_lds<false>(kl, vkey0(1), a.Sk, kt0 + TILE, w);
+  }
+
+  // Q^T operand: k-step st covers head_dim 16 st + 8 g .. +7 of the row
+  u32x4 qf[8];
+  auto load_q = [&](int qb) {
+    const int row = qb * BM + w * 32 + lq;
+#pragma unroll
+    for (int st = 0; st < 8; ++st)
+      qf[st] = row < a.Sq ? *(const u32x4 *)(qp + row * a.qs2 + 16 * st + 8 * g)
+                          : u32x4{0, 0, 0, 0};
+  };
+  load_q(qbs[0]);
 
   // per-lane LDS byte offsets of the operand reads
   int ka[8];  // K: row lq (+32 kb), logical unit 2 st + g
@@ -146,41 +202,83 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a) {
   }
 
   f32x16 o[4];
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[nb][r] = 0.0f;
   f32x16 s[2];
-  float m = kNegFltMax, lsum = 0.0f;
+  float m, lsum;
+  auto reset = [&]() {
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[nb][r] = 0.0f;
+    m = kNegFltMax;
+    lsum = 0.0f;
+  };
+  reset();
   const float sc = a.scale2;
   const f32x16 zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
-  wait_vmem();
-  __syncthreads();
-  if (nkw > 0) {
+  auto qk = [&](const uint8_t *kt) {
 #pragma unroll
     for (int st = 0; st < 8; ++st)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const u32x4 A = *(const u32x4 *)(kt0 + kb * 8192 + ka[st]);
+        const u32x4 A = *(const u32x4 *)(kt + kb * 8192 + ka[st]);
         s[kb] = E::mfma32(as_vec8<V8>(A), as_vec8<V8>(qf[st]), st == 0 ? zero16 : s[kb]);
       }
-  }
+    // operand reads run two MFMAs ahead (bounds the live registers)
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+#pragma unroll
+    for (int i = 0; i < 14; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
+  };
+
+  // O = acc / l rounded to the input type (HTile:130-143) and the LSE
+  auto finalize = [&](int qb) {
+    const float ltot = pair_sum(lsum);
+    const int row = qb * BM + w * 32 + lq;
+    if (row < a.Sq) {
+      const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
+      uint16_t *op = (uint16_t *)a.o + b * a.os0 + h * a.os1 + row * a.os2;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const u32x2 pk = {E::pack2(o[nb][4 * rq] * inv, o[nb][4 * rq + 1] * inv),
+                            E::pack2(o[nb][4 * rq + 2] * inv, o[nb][4 * rq + 3] * inv)};
+          *(u32x2 *)(op + 32 * nb + 8 * rq + 4 * g) = pk;
+        }
+      if (g == 0 && a.lse)
+        a.lse[((int64_t)b * a.Hq + h) * a.Sq + row] =
+            ltot > 0.0f ? (m + log2f(ltot)) * kLn2 : -INFINITY;
+    }
+  };
+
+  wait_vmem();
+  __syncthreads();
+  if (nkw[0] > 0) qk(kt0);
   __syncthreads();  // every wave is done with K slot 0 before it is refilled
 
-  for (int jb = 0; jb < nkb; ++jb) {
-    if (jb + 2 < nkb) tile_to_lds<false>(kp, a.ks2, (jb + 2) * BN, a.Sk, kt0 + (jb & 1) * TILE, w, lane);
-    if (jb + 1 < nkb) tile_to_lds<true>(vp, a.vs2, (jb + 1) * BN, a.Sk, vt0 + ((jb + 1) & 1) * TILE, w, lane);
-    if (jb < nkw) {
+  for (int vb = 0; vb < nv; ++vb) {
+    const int item = vb >= n0 ? 1 : 0;
+    const int jb = vb - item * n0;  // key block within the query block
+    if (vb + 2 < nv) tile_to_lds<false>(kl, vkey0(vb + 2), a.Sk, kt0 + (vb & 1) * TILE, w);
+    if (vb + 1 < nv) tile_to_lds<true>(vl, vkey0(vb + 1), a.Sk, vt0 + ((vb + 1) & 1) * TILE, w);
+    // q0's last block: Q^T of q1 loads while the block is consumed (this
+    // wave's last QK^T of q0 was issued one block earlier)
+    if (vb == n0 - 1 && nkb[1] > 0) load_q(qbs[1]);
+    const int qrow0 = qbs[item] * BM + w * 32;
+    if (jb < nkw[item]) {
       const int key0 = jb * BN;
-      const bool need_mask = (key0 + BN > a.Sk) || (CAUSAL && key0 + BN - 1 > row0 + a.off);
+      const bool need_mask = (key0 + BN > a.Sk) || (CAUSAL && key0 + BN - 1 > qrow0 + a.off);
       if (need_mask) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int key = key0 + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3);
-            if (key >= a.Sk || (CAUSAL && key > row + a.off)) s[kb][r] = -INFINITY;
+            if (key >= a.Sk || (CAUSAL && key > qrow0 + lq + a.off)) s[kb][r] = -INFINITY;
           }
       }
       float mx = -INFINITY;
@@ -223,7 +321,7 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a) {
       lsum += rs;
 
       // O^T += V^T P^T for this block (A operand by transpose reads)
-      const uint8_t *vt = vt0 + (jb & 1) * TILE;
+      const uint8_t *vt = vt0 + (vb & 1) * TILE;
 #pragma unroll
       for (int step = 0; step < 16; ++step) {
         const int c = step >> 2, nb = step & 3;
@@ -244,54 +342,32 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a) {
       }
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
 
-      // S^T of the next block (its K tile arrived during the previous iteration)
-      if (jb + 1 < nkw) {
-        const uint8_t *kt = kt0 + ((jb + 1) & 1) * TILE;
-#pragma unroll
-        for (int st = 0; st < 8; ++st)
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb) {
-            const u32x4 A = *(const u32x4 *)(kt + kb * 8192 + ka[st]);
-            s[kb] = E::mfma32(as_vec8<V8>(A), as_vec8<V8>(qf[st]), st == 0 ? zero16 : s[kb]);
-          }
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
-#pragma unroll
-        for (int i = 0; i < 14; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
-      }
+      // S^T of the next block of this query block (its K tile arrived
+      // during the previous iteration)
+      if (jb + 1 < nkw[item]) qk(kt0 + ((vb + 1) & 1) * TILE);
     }
     wait_vmem();
     __syncthreads();
+    if (vb == n0 - 1) {
+      // switch to q1: its Q^T has landed, its first K tile too
+      finalize(qbs[0]);
+      reset();
+      if (nkw[1] > 0) qk(kt0 + ((vb + 1) & 1) * TILE);
+      __syncthreads();  // that K slot is refilled by the next iteration
+    }
   }
-
-  const float ltot = pair_sum(lsum);
-  if (row < a.Sq) {
-    const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
-    uint16_t *op = (uint16_t *)a.o + b * a.os0 + h * a.os1 + row * a.os2;
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const u32x2 pk = {E::pack2(o[nb][4 * rq] * inv, o[nb][4 * rq + 1] * inv),
-                          E::pack2(o[nb][4 * rq + 2] * inv, o[nb][4 * rq + 3] * inv)};
-        *(u32x2 *)(op + 32 * nb + 8 * rq + 4 * g) = pk;
-      }
-    if (g == 0 && a.lse)
-      a.lse[((int64_t)b * a.Hq + h) * a.Sq + row] =
-          ltot > 0.0f ? (m + log2f(ltot)) * kLn2 : -INFINITY;
-  }
+  if (n0 == 0) finalize(qbs[0]);  // no visible keys: O = 0, LSE = -inf
+  if (two) finalize(qbs[1]);
 }
 
 template <class E>
 void launch_t(const AttnArgs &a, bool causal, hipStream_t s) {
-  const dim3 grid((unsigned)(a.nqb * a.BH));
+  const int npair = (a.nqb + 1) / 2;
+  const dim3 grid((unsigned)(npair * a.BH));
   if (causal)
-    hipLaunchKernelGGL((attn_fwd_d128<E, true>), grid, dim3(NT), 0, s, a);
+    hipLaunchKernelGGL((attn_fwd_d128<E, true>), grid, dim3(NT), 0, s, a, npair);
   else
-    hipLaunchKernelGGL((attn_fwd_d128<E, false>), grid, dim3(NT), 0, s, a);
+    hipLaunchKernelGGL((attn_fwd_d128<E, false>), grid, dim3(NT), 0, s, a, npair);
 }
 
 }  // namespace
