@@ -79,23 +79,48 @@ __device__ inline TileLoader make_loader(const uint16_t *src, int64_t stride, in
   return t;
 }
 
+// One global_load_lds_dwordx4 (16 bytes per lane into LDS at lds_addr +
+// 16 * lane). Issued as inline assembly: the compiler's wait-count pass does
+// not order ds_read_b64_tr_b16 against LDS DMA by address and would put a
+// full vmcnt(0) drain before every transpose read, serialising the prefetch.
+// Completion is awaited explicitly (wait_vmem + barrier) before any wave
+// reads a refilled slot.
+__device__ inline void dma16(const char *sbase, uint32_t voff, uint32_t lds_addr) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(voff), "s"(sbase), "s"(lds_addr)
+      : "memory", "m0");
+}
+__device__ inline void dma16(const char *addr, uint32_t lds_addr) {
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(addr), "s"(lds_addr)
+      : "memory", "m0");
+}
+__device__ inline uint32_t lds_offset(const uint8_t *p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)as_lds(p));
+}
+
 template <bool IS_V>
 __device__ inline void tile_to_lds(const TileLoader &t, int key0, int Sk, const uint8_t *tile,
                                    int w) {
   if (key0 + BN <= Sk) {
     const char *blk = t.base + (int64_t)key0 * t.row_bytes;
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-      __builtin_amdgcn_global_load_lds(blk + t.off[c], as_lds(tile + (4 * w + c) * 1024), 16, 0,
-                                       0);
+    for (int c = 0; c < 4; ++c) dma16(blk, t.off[c], lds_offset(tile + (4 * w + c) * 1024));
   } else {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int r = t.lane_row + 4 * c;
       const int unit = t.sw_base ^ (IS_V ? ((r & 3) << 2) : (r & 15));
       const int key = min(key0 + r, Sk - 1);
-      __builtin_amdgcn_global_load_lds(t.base + (int64_t)key * t.row_bytes + unit * 16,
-                                       as_lds(tile + (4 * w + c) * 1024), 16, 0, 0);
+      dma16(t.base + (int64_t)key * t.row_bytes + unit * 16, lds_offset(tile + (4 * w + c) * 1024));
     }
   }
 }
@@ -265,9 +290,6 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a, int npair) {
     const int jb = vb - item * n0;  // key block within the query block
     if (vb + 2 < nv) tile_to_lds<false>(kl, vkey0(vb + 2), a.Sk, kt0 + (vb & 1) * TILE, w);
     if (vb + 1 < nv) tile_to_lds<true>(vl, vkey0(vb + 1), a.Sk, vt0 + ((vb + 1) & 1) * TILE, w);
-    // q0's last block: Q^T of q1 loads while the block is consumed (this
-    // wave's last QK^T of q0 was issued one block earlier)
-    if (vb == n0 - 1 && nkb[1] > 0) load_q(qbs[1]);
     const int qrow0 = qbs[item] * BM + w * 32;
     if (jb < nkw[item]) {
       const int key0 = jb * BN;
@@ -349,9 +371,16 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a, int npair) {
     wait_vmem();
     __syncthreads();
     if (vb == n0 - 1) {
-      // switch to q1: its Q^T has landed, its first K tile too
+      // switch to q1 (its first K tile has landed): load its Q^T here, not
+      // earlier, so no load into the Q^T registers is ever pending inside
+      // the steady-state loop (that would make every QK^T drain the K/V
+      // prefetch along with it)
       finalize(qbs[0]);
       reset();
+      if (nkb[1] > 0) {
+        load_q(qbs[1]);
+        wait_vmem();
+      }
       if (nkw[1] > 0) qk(kt0 + ((vb + 1) & 1) * TILE);
       __syncthreads();  // that K slot is refilled by the next iteration
     }
