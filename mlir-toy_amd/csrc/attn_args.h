@@ -19,7 +19,4 @@ struct AttnArgs {
 // Launches the head_dim-128 16-bit kernel (attn_fwd_d128.hip); dtype 1 = f16, 2 = bf16.
 hipError_t launch_attn_d128(const AttnArgs &a, int32_t dtype, bool causal, hipStream_t s);
 
-// Launches the head_dim-128 16-bit ping-pong kernel (attn_fwd_pp.hip).
-hipError_t launch_attn_pp(const AttnArgs &a, int32_t dtype, bool causal, hipStream_t s);
-
 }  // namespace neptune

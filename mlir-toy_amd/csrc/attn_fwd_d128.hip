@@ -85,23 +85,37 @@ __device__ inline TileLoader make_loader(const uint16_t *src, int64_t stride, in
 // full vmcnt(0) drain before every transpose read, serialising the prefetch.
 // Completion is awaited explicitly (wait_vmem + barrier) before any wave
 // reads a refilled slot.
+// M0 is saved and restored around the DMA: the compiler treats M0 as
+// reserved and does not honour it as a clobber.
+__device__ inline const char *uniform_ptr(const char *p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const char *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
 __device__ inline void dma16(const char *sbase, uint32_t voff, uint32_t lds_addr) {
+  uint32_t saved;
   asm volatile(
-      "s_mov_b32 m0, %2\n\t"
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %0, %1"
-      :
-      : "v"(voff), "s"(sbase), "s"(lds_addr)
-      : "memory", "m0");
+      "global_load_lds_dwordx4 %1, %2\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(uniform_ptr(sbase)), "s"(lds_addr)
+      : "memory");
 }
 __device__ inline void dma16(const char *addr, uint32_t lds_addr) {
+  uint32_t saved;
   asm volatile(
-      "s_mov_b32 m0, %1\n\t"
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %0, off"
-      :
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
       : "v"(addr), "s"(lds_addr)
-      : "memory", "m0");
+      : "memory");
 }
 __device__ inline uint32_t lds_offset(const uint8_t *p) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)as_lds(p));
@@ -342,7 +356,10 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a, int npair) {
       }
       lsum += rs;
 
-      // O^T += V^T P^T for this block (A operand by transpose reads)
+      // O^T += V^T P^T for this block (A operand by transpose reads). The
+      // wave raises its issue priority for its MFMA stretch so the matrix
+      // core is fed first while the other wave on the SIMD runs its softmax.
+      __builtin_amdgcn_s_setprio(1);
       const uint8_t *vt = vt0 + (vb & 1) * TILE;
 #pragma unroll
       for (int step = 0; step < 16; ++step) {
@@ -367,6 +384,7 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a, int npair) {
       // S^T of the next block of this query block (its K tile arrived
       // during the previous iteration)
       if (jb + 1 < nkw[item]) qk(kt0 + ((vb + 1) & 1) * TILE);
+      __builtin_amdgcn_s_setprio(0);
     }
     wait_vmem();
     __syncthreads();
