@@ -32,6 +32,7 @@
 #include "attn_args.h"
 #include "device_common.h"
 #include "kernels.h"
+#include "lds_dma.h"
 
 namespace neptune {
 namespace {
@@ -42,12 +43,6 @@ constexpr int HD = 128;
 constexpr int NT = 256;
 constexpr int TILE = BN * HD * 2;  // bytes per K or V tile (16 KiB)
 constexpr float kSlack = 8.0f;     // lazy-rescale threshold (log2 units)
-
-typedef short v4i16 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-
-__device__ inline lds_void *as_lds(const uint8_t *p) { return (lds_void *)(p); }
 
 // Wave w copies rows [16w, 16w+16) of a 64 x 128 tile (four 1 KiB chunks of
 // four rows) straight into LDS. Full blocks take a wave-uniform base pointer
@@ -77,48 +72,6 @@ __device__ inline TileLoader make_loader(const uint16_t *src, int64_t stride, in
     t.off[c] = (uint32_t)((int64_t)r * t.row_bytes + unit * 16);
   }
   return t;
-}
-
-// One global_load_lds_dwordx4 (16 bytes per lane into LDS at lds_addr +
-// 16 * lane). Issued as inline assembly: the compiler's wait-count pass does
-// not order ds_read_b64_tr_b16 against LDS DMA by address and would put a
-// full vmcnt(0) drain before every transpose read, serialising the prefetch.
-// Completion is awaited explicitly (wait_vmem + barrier) before any wave
-// reads a refilled slot.
-// M0 is saved and restored around the DMA: the compiler treats M0 as
-// reserved and does not honour it as a clobber.
-__device__ inline const char *uniform_ptr(const char *p) {
-  const uint64_t v = (uint64_t)(uintptr_t)p;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return (const char *)(uintptr_t)(((uint64_t)hi << 32) | lo);
-}
-__device__ inline void dma16(const char *sbase, uint32_t voff, uint32_t lds_addr) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %3\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, %2\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(voff), "s"(uniform_ptr(sbase)), "s"(lds_addr)
-      : "memory");
-}
-__device__ inline void dma16(const char *addr, uint32_t lds_addr) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %2\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(addr), "s"(lds_addr)
-      : "memory");
-}
-__device__ inline uint32_t lds_offset(const uint8_t *p) {
-  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)as_lds(p));
 }
 
 template <bool IS_V>

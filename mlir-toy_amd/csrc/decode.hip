@@ -32,6 +32,7 @@
 // block is a multiple of 32 and every wave range starts on a 32 boundary).
 #include "device_common.h"
 #include "kernels.h"
+#include "lds_dma.h"
 
 namespace neptune {
 namespace {
@@ -313,6 +314,218 @@ __global__ __launch_bounds__(DT, 2) void decode_partial(DecArgs a) {
   }
 }
 
+// bf16 KV through LDS: each wave streams its token range in 32-token steps
+// through a private two-slot ring (K and V tiles of 32 x 128 bf16, 8 KiB
+// each) filled by global_load_lds_dwordx4, one step ahead of use. The K tile
+// feeds S^T = K.Q^T (v_mfma_f32_16x16x32_bf16, A = K rows by ds_read_b128),
+// the V tile feeds O^T += V^T.P^T with A read by ds_read_b64_tr_b16. No
+// data passes through VGPRs on its way to LDS and no vector ALU work is
+// spent on transposing V.
+//   K tile: unit u of token row r at u ^ (r & 15)      (16 rows per read)
+//   V tile: unit u of token row r at u ^ 2 (r & 7)     (transpose reads of
+//           rows 0-15 or 16-31, 32 bytes each)
+constexpr int RSTEP = 32;                   // tokens per step
+constexpr int RTILE = RSTEP * DH * 2;       // bytes of one K or V tile
+constexpr int RSLOT = 2 * RTILE;            // K + V
+constexpr int RWAVE = 2 * RSLOT;            // two slots per wave
+constexpr int RW = 2;                       // waves per work-group
+constexpr int RT = 64 * RW;                 // threads per work-group
+constexpr int RLDS = RW * RWAVE;            // two work-groups fit one CU
+
+__global__ __launch_bounds__(RT) void decode_partial_ring(DecArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, G = lane >> 4;  // MFMA column (query head) / lane group
+  const int id = blockIdx.x;
+  const int split = id % a.splits;
+  const int bk = id / a.splits;  // batch * Hk + kv head
+  const int b = bk / a.Hk, hk = bk % a.Hk;
+  const int Gq = a.group;
+
+  const int c0 = split * a.chunk;
+  const int c1 = min(c0 + a.chunk, a.L);
+  const int wlen = ((a.chunk + RW * RSTEP - 1) / (RW * RSTEP)) * RSTEP;
+  const int t0 = c0 + w * wlen;
+  const int t1 = min(t0 + wlen, c1);
+  const int nsteps = t1 > t0 ? (t1 - t0 + RSTEP - 1) / RSTEP : 0;
+
+  const uint8_t *ring = smem + w * RWAVE;
+  const char *kbase = (const char *)a.k + (int64_t)bk * a.L * DH * 2;
+  const char *vbase = (const char *)a.v + (int64_t)bk * a.L * DH * 2;
+  // per-lane byte offsets of this lane's 16 bytes in DMA chunk c (rows 4c + G)
+  uint32_t koff[8], voff[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int r = 4 * c + G;
+    koff[c] = (uint32_t)(r * DH * 2 + (((lane & 15) ^ (r & 15)) << 4));
+    voff[c] = (uint32_t)(r * DH * 2 + (((lane & 15) ^ (2 * (r & 7))) << 4));
+  }
+  auto issue = [&](int i) {
+    const int tb = t0 + i * RSTEP;
+    const uint8_t *slot = ring + (i & 1) * RSLOT;
+    if (tb + RSTEP <= a.L) {
+      const char *kb = kbase + (int64_t)tb * DH * 2, *vb = vbase + (int64_t)tb * DH * 2;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) dma16<true>(kb, koff[c], lds_offset(slot + c * 1024));
+#pragma unroll
+      for (int c = 0; c < 8; ++c) dma16<true>(vb, voff[c], lds_offset(slot + RTILE + c * 1024));
+    } else {  // tail: rows past the sequence re-read the last token (masked)
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const int r = 4 * c + G;
+        const int64_t row = min(tb + r, a.L - 1);
+        dma16<true>(kbase + row * DH * 2 + (((lane & 15) ^ (r & 15)) << 4),
+              lds_offset(slot + c * 1024));
+      }
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const int r = 4 * c + G;
+        const int64_t row = min(tb + r, a.L - 1);
+        dma16<true>(vbase + row * DH * 2 + (((lane & 15) ^ (2 * (r & 7))) << 4),
+              lds_offset(slot + RTILE + c * 1024));
+      }
+    }
+  };
+  if (nsteps > 0) issue(0);
+  if (nsteps > 1) issue(1);
+
+  // Q^T operand: k-step ks covers head_dim 32 ks + 8 G .. +7 of head n
+  u32x4 qf[4];
+  {
+    const uint16_t *qrow = a.q + ((int64_t)b * a.Hq + hk * Gq + n) * DH;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      qf[ks] = n < Gq ? *(const u32x4 *)(qrow + 32 * ks + 8 * G) : u32x4{0, 0, 0, 0};
+  }
+  // LDS read offsets: K A-operand (row n of each 16-key half, unit 4 ks + G),
+  // V^T transpose reads (rows 4 G + i, columns 16 mb + 4 q)
+  int ka[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) ka[ks] = n * 256 + (((4 * ks + G) ^ n) << 4);
+  const int vi = (lane & 15) >> 2, vq = lane & 3;
+  const int vrow = 4 * G + vi;
+
+  f32x4 oacc[8];
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb) oacc[mb] = f32x4{0, 0, 0, 0};
+  float m = kNegFltMax, lsum = 0.0f;
+  const float sc = a.scale2;
+
+  for (int i = 0; i < nsteps; ++i) {
+    // this step's tiles have landed once only the next step's 16 copies
+    // may still be outstanding
+    if (i + 1 < nsteps)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(16));
+    else
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    const uint8_t *kt = ring + (i & 1) * RSLOT;
+    const uint8_t *vt = kt + RTILE;
+    const int t = t0 + i * RSTEP;
+
+    f32x4 s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      s[kb] = f32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const u32x4 A = *(const u32x4 *)(kt + kb * 4096 + ka[ks]);
+        s[kb] = Bf16Tag::mfma16(as_vec8<bf16x8>(A), as_vec8<bf16x8>(qf[ks]), s[kb]);
+      }
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[kb][r] *= sc;
+    if (t + RSTEP > t1) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (t + 16 * kb + 4 * G + r >= t1) s[kb][r] = -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kb][r]);
+    mx = wave_max_xor(mx, 16);
+    mx = wave_max_xor(mx, 32);
+    const float m_new = fmaxf(m, mx);
+    const float alpha = fast_exp2(m - m_new);
+    float rs = 0.0f;
+    float p[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float e = fast_exp2(s[j >> 2][j & 3] - m_new);
+      rs += e;
+      p[j] = e;
+    }
+    lsum = lsum * alpha + rs;
+    m = m_new;
+    if (__any(alpha != 1.0f)) {
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) oacc[mb][r] *= alpha;
+    }
+    // P^T: k-slot 8 G + j holds key 4 G + j (j < 4) or 16 + 4 G + j - 4
+    u32x4 pf;
+#pragma unroll
+    for (int i2 = 0; i2 < 4; ++i2) pf[i2] = Bf16Tag::pack2(p[2 * i2], p[2 * i2 + 1]);
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      const int col = 32 * (mb ^ (vrow & 7)) + 8 * vq;
+      const v4i16 lo = lds_read_tr16(vt + vrow * 256 + col);
+      const v4i16 hi = lds_read_tr16(vt + (vrow + 16) * 256 + col);
+      const u32x2 a0 = __builtin_bit_cast(u32x2, lo), a1 = __builtin_bit_cast(u32x2, hi);
+      const u32x4 A = {a0[0], a0[1], a1[0], a1[1]};
+      oacc[mb] = Bf16Tag::mfma16(as_vec8<bf16x8>(A), as_vec8<bf16x8>(pf), oacc[mb]);
+    }
+    // every read of this slot has returned before it is refilled
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    if (i + 2 < nsteps) issue(i + 2);
+  }
+
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
+
+  // ---- merge the waves of this split
+  __syncthreads();
+  float *mo = (float *)smem;              // [RW][16][DH]
+  float *mml = mo + RW * 16 * DH;         // [RW][16][2]
+  if (n < Gq) {
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mo[(w * 16 + n) * DH + 16 * mb + 4 * G + r] = oacc[mb][r];
+    if (G == 0) {
+      mml[(w * 16 + n) * 2 + 0] = m;
+      mml[(w * 16 + n) * 2 + 1] = lsum;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < Gq * DH; e += RT) {
+    const int hn = e / DH, d = e % DH;
+    float M = kNegFltMax;
+#pragma unroll
+    for (int ww = 0; ww < RW; ++ww) M = fmaxf(M, mml[(ww * 16 + hn) * 2]);
+    float acc = 0.0f, Ls = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < RW; ++ww) {
+      const float wgt = fast_exp2(mml[(ww * 16 + hn) * 2] - M);
+      acc += wgt * mo[(ww * 16 + hn) * DH + d];
+      Ls += wgt * mml[(ww * 16 + hn) * 2 + 1];
+    }
+    const int64_t row = ((int64_t)b * a.Hq + hk * Gq + hn) * a.splits + split;
+    a.part_o[row * DH + d] = acc;
+    if (d == 0) {
+      a.part_ml[row * 2 + 0] = M;
+      a.part_ml[row * 2 + 1] = Ls;
+    }
+  }
+}
+
 // One work-group per (batch, query head): combine the splits' partials.
 __global__ __launch_bounds__(DH) void decode_combine(const float *part_o,
                                                      const float *part_ml,
@@ -401,10 +614,18 @@ hipError_t launch_decode(const DecodeLaunch &L, hipStream_t s) {
   a.sb = (int32_t)L.scale_block;
   a.scale2 = L.scale_log2;
   const int grid = (int)(L.batch * L.heads_kv * L.splits);
-  if (L.kv_dtype == 3)
+  if (L.kv_dtype == 3) {
     hipLaunchKernelGGL(decode_partial<true>, dim3(grid), dim3(DT), 0, s, a);
-  else
-    hipLaunchKernelGGL(decode_partial<false>, dim3(grid), dim3(DT), 0, s, a);
+  } else {
+    static bool attr_set = false;  // benign race: the attribute is idempotent
+    if (!attr_set) {
+      hipError_t e = hipFuncSetAttribute((const void *)decode_partial_ring,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, RLDS);
+      if (e != hipSuccess) return e;
+      attr_set = true;
+    }
+    hipLaunchKernelGGL(decode_partial_ring, dim3(grid), dim3(RT), RLDS, s, a);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(decode_combine, dim3((unsigned)(L.batch * L.heads_q)), dim3(DH), 0, s,

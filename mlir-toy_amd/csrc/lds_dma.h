@@ -1,0 +1,98 @@
+// lds_dma.h — HBM -> LDS copies on gfx950 (global_load_lds_dwordx4) and the
+// LDS pointer helpers the tiled kernels share.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace neptune {
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
+__device__ inline lds_void *as_lds(const uint8_t *p) { return (lds_void *)(p); }
+
+// ds_read_b64_tr_b16 of the 8 bytes at p (LDS)
+__device__ inline v4i16 lds_read_tr16(const uint8_t *p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)as_lds(p));
+}
+
+__device__ inline const char *uniform_ptr(const char *p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const char *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ inline uint32_t lds_offset(const uint8_t *p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)as_lds(p));
+}
+
+// One global_load_lds_dwordx4: 16 bytes per lane into LDS at lds_addr +
+// 16 * lane. Issued as inline assembly because the compiler's wait-count
+// pass does not order ds_read_b64_tr_b16 against LDS DMA by address and
+// would drain every outstanding load (vmcnt(0)) before each transpose read,
+// serialising any prefetch. The compiler therefore does not count these
+// loads: callers wait for them explicitly (s_waitcnt vmcnt, plus a barrier
+// when other waves read the data) and finish their own reads of a slot
+// (lgkmcnt(0)) before refilling it. M0 is saved and restored around the
+// copy because the compiler treats it as reserved, not as a clobber.
+// NT = true marks the load non-temporal (streamed data read once: keeps it
+// from displacing reused lines, and measured on MI355X it sustains ~7.1 TB/s
+// against ~6.4 TB/s for plain loads).
+template <bool NT = false>
+__device__ inline void dma16(const char *sbase, uint32_t voff, uint32_t lds_addr) {
+  uint32_t saved;
+  if (NT)
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2 nt\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(voff), "s"(uniform_ptr(sbase)), "s"(lds_addr)
+        : "memory");
+  else
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(voff), "s"(uniform_ptr(sbase)), "s"(lds_addr)
+        : "memory");
+}
+template <bool NT = false>
+__device__ inline void dma16(const char *addr, uint32_t lds_addr) {
+  uint32_t saved;
+  if (NT)
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, off nt\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(addr), "s"(lds_addr)
+        : "memory");
+  else
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(addr), "s"(lds_addr)
+        : "memory");
+}
+
+// s_waitcnt immediates (gfx9 encoding): wait until at most n vector-memory
+// operations are outstanding / until all LDS operations have completed.
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int kWaitLgkm0 = 0xc07f;
+
+}  // namespace neptune
