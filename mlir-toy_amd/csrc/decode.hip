@@ -118,7 +118,7 @@ __global__ __launch_bounds__(DT, 2) void decode_partial(DecArgs a) {
         const uint8_t *kp = (const uint8_t *)a.k + kvbase + (int64_t)key * DH;
 #pragma unroll
         for (int sp = 0; sp < 2; ++sp)
-          kr[2 * kb + sp] = *(const u32x4 *)(kp + 64 * sp + 16 * g);
+          kr[2 * kb + sp] = __builtin_nontemporal_load((const u32x4 *)(kp + 64 * sp + 16 * g));
       } else {
         const uint16_t *kp = (const uint16_t *)a.k + kvbase + (int64_t)key * DH;
 #pragma unroll
@@ -133,7 +133,7 @@ __global__ __launch_bounds__(DT, 2) void decode_partial(DecArgs a) {
       int key = min(t + 4 * kq + i, a.L - 1);
       if (FP8) {
         const uint8_t *vp = (const uint8_t *)a.v + kvbase + (int64_t)key * DH;
-        vr[i] = *(const u32x4 *)(vp + 16 * dc);
+        vr[i] = __builtin_nontemporal_load((const u32x4 *)(vp + 16 * dc));
       } else {
         const uint16_t *vp = (const uint16_t *)a.v + kvbase + (int64_t)key * DH;
 #pragma unroll
