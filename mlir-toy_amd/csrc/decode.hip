@@ -526,6 +526,223 @@ __global__ __launch_bounds__(RT) void decode_partial_ring(DecArgs a) {
   }
 }
 
+// fp8-E4M3 KV through LDS, the same ring design as decode_partial_ring with
+// 1-byte codes: K and V tiles of 32 tokens x 128 B (4 KiB) per slot, filled
+// by non-temporal global_load_lds_dwordx4. Codes are widened to bf16 in
+// registers (exact); the per-(token block) K scale folds into the score
+// scale and the V scale into P before its bf16 rounding. 32-token steps
+// never straddle a scale block (the block is a multiple of 32 and every
+// wave range starts on a 32-token boundary).
+//   K tile: 16-byte unit u of row r at u ^ ((r >> 1) & 7); a lane reads the
+//           16 codes of head_dim 64 sp + 16 G .. +15 (two MFMA k-steps).
+//   V tile: same layout; V^T comes from ds_read_b64_tr_b8, whose source
+//           lane pair (2i, 2i+1) names the token row of k-slot i, so the
+//           rows can follow the P^T key order directly.
+constexpr int R8TILE = RSTEP * DH;          // bytes of one K or V code tile
+constexpr int R8SLOT = 2 * R8TILE;
+constexpr int R8WAVE = 2 * R8SLOT;
+constexpr int R8LDS = RW * R8WAVE;
+
+typedef int v2i32 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i32 lds_v2i32;
+
+__global__ __launch_bounds__(RT) void decode_partial_ring8(DecArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, G = lane >> 4;
+  const int id = blockIdx.x;
+  const int split = id % a.splits;
+  const int bk = id / a.splits;
+  const int b = bk / a.Hk, hk = bk % a.Hk;
+  const int Gq = a.group;
+
+  const int c0 = split * a.chunk;
+  const int c1 = min(c0 + a.chunk, a.L);
+  const int wlen = ((a.chunk + RW * RSTEP - 1) / (RW * RSTEP)) * RSTEP;
+  const int t0 = c0 + w * wlen;
+  const int t1 = min(t0 + wlen, c1);
+  const int nsteps = t1 > t0 ? (t1 - t0 + RSTEP - 1) / RSTEP : 0;
+
+  const uint8_t *ring = smem + w * R8WAVE;
+  const char *kbase = (const char *)a.k + (int64_t)bk * a.L * DH;
+  const char *vbase = (const char *)a.v + (int64_t)bk * a.L * DH;
+  // DMA chunk c covers rows 8c .. 8c+7; this lane moves row 8c + lane/8,
+  // physical unit lane & 7
+  uint32_t off[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int r = 8 * c + (lane >> 3);
+    off[c] = (uint32_t)(r * DH + (((lane & 7) ^ ((r >> 1) & 7)) << 4));
+  }
+  auto issue = [&](int i) {
+    const int tb = t0 + i * RSTEP;
+    const uint8_t *slot = ring + (i & 1) * R8SLOT;
+    if (tb + RSTEP <= a.L) {
+      const char *kb = kbase + (int64_t)tb * DH, *vb = vbase + (int64_t)tb * DH;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) dma16<true>(kb, off[c], lds_offset(slot + c * 1024));
+#pragma unroll
+      for (int c = 0; c < 4; ++c) dma16<true>(vb, off[c], lds_offset(slot + R8TILE + c * 1024));
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int r = 8 * c + (lane >> 3);
+        const int64_t row = min(tb + r, a.L - 1);
+        const int u = ((lane & 7) ^ ((r >> 1) & 7)) << 4;
+        dma16<true>(kbase + row * DH + u, lds_offset(slot + c * 1024));
+        dma16<true>(vbase + row * DH + u, lds_offset(slot + R8TILE + c * 1024));
+      }
+    }
+  };
+  if (nsteps > 0) issue(0);
+  if (nsteps > 1) issue(1);
+
+  // Q^T operand: k-step ks covers head_dim 64 (ks >> 1) + 16 G + 8 (ks & 1) .. +7
+  u32x4 qf[4];
+  {
+    const uint16_t *qrow = a.q + ((int64_t)b * a.Hq + hk * Gq + n) * DH;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int d = 64 * (ks >> 1) + 16 * G + 8 * (ks & 1);
+      qf[ks] = n < Gq ? *(const u32x4 *)(qrow + d) : u32x4{0, 0, 0, 0};
+    }
+  }
+  // K reads: row n (+16 kb), logical unit 4 sp + G
+  int ka[2];
+#pragma unroll
+  for (int sp = 0; sp < 2; ++sp) ka[sp] = n * DH + (((4 * sp + G) ^ ((n >> 1) & 7)) << 4);
+  // V^T reads: source lane pair (2i, 2i+1) of group G names the token row of
+  // k-slot i (keys 4 G + i, then 16 + 4 G + i - 4), 8 bytes each
+  const int vi = (lane & 15) >> 1, vhalf = lane & 1;
+  const int vrow = (vi < 4 ? 4 * G + vi : 16 + 4 * G + vi - 4);
+  const int vrow_off = vrow * DH + 8 * vhalf;
+  const int vsw = (vrow >> 1) & 7;
+
+  f32x4 oacc[8];
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb) oacc[mb] = f32x4{0, 0, 0, 0};
+  float m = kNegFltMax, lsum = 0.0f;
+
+  for (int i = 0; i < nsteps; ++i) {
+    if (i + 1 < nsteps)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(8));
+    else
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    const uint8_t *kt = ring + (i & 1) * R8SLOT;
+    const uint8_t *vt = kt + R8TILE;
+    const int t = t0 + i * RSTEP;
+
+    f32x4 s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      s[kb] = f32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int sp = 0; sp < 2; ++sp) {
+        const u32x4 c = *(const u32x4 *)(kt + kb * 16 * DH + ka[sp]);
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const u32x2 lo = e4m3x4_to_bf16(c[2 * h2]);
+          const u32x2 hi = e4m3x4_to_bf16(c[2 * h2 + 1]);
+          const u32x4 A = {lo[0], lo[1], hi[0], hi[1]};
+          s[kb] = Bf16Tag::mfma16(as_vec8<bf16x8>(A), as_vec8<bf16x8>(qf[2 * sp + h2]), s[kb]);
+        }
+      }
+    }
+    const int blk = t / a.sb;
+    const float sc = a.scale2 * a.ksc[(int64_t)bk * a.nsb + blk];
+    const float vsc = a.vsc[(int64_t)bk * a.nsb + blk];
+    // scale first, then mask: a zero fp8 scale must not meet -inf
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[kb][r] *= sc;
+    if (t + RSTEP > t1) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (t + 16 * kb + 4 * G + r >= t1) s[kb][r] = -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kb][r]);
+    mx = wave_max_xor(mx, 16);
+    mx = wave_max_xor(mx, 32);
+    const float m_new = fmaxf(m, mx);
+    const float alpha = fast_exp2(m - m_new);
+    float rs = 0.0f;
+    float p[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float e = fast_exp2(s[j >> 2][j & 3] - m_new);
+      rs += e;
+      p[j] = e;
+    }
+    lsum = lsum * alpha + rs;
+    m = m_new;
+    if (__any(alpha != 1.0f)) {
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) oacc[mb][r] *= alpha;
+    }
+    u32x4 pf;
+#pragma unroll
+    for (int i2 = 0; i2 < 4; ++i2) pf[i2] = Bf16Tag::pack2(p[2 * i2] * vsc, p[2 * i2 + 1] * vsc);
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      const v2i32 c = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+          (lds_v2i32 *)as_lds(vt + vrow_off + ((mb ^ vsw) << 4)));
+      const u32x2 lo = e4m3x4_to_bf16((uint32_t)c[0]);
+      const u32x2 hi = e4m3x4_to_bf16((uint32_t)c[1]);
+      const u32x4 A = {lo[0], lo[1], hi[0], hi[1]};
+      oacc[mb] = Bf16Tag::mfma16(as_vec8<bf16x8>(A), as_vec8<bf16x8>(pf), oacc[mb]);
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    if (i + 2 < nsteps) issue(i + 2);
+  }
+
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
+
+  __syncthreads();
+  float *mo = (float *)smem;              // [RW][16][DH]
+  float *mml = mo + RW * 16 * DH;         // [RW][16][2]
+  if (n < Gq) {
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mo[(w * 16 + n) * DH + 16 * mb + 4 * G + r] = oacc[mb][r];
+    if (G == 0) {
+      mml[(w * 16 + n) * 2 + 0] = m;
+      mml[(w * 16 + n) * 2 + 1] = lsum;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < Gq * DH; e += RT) {
+    const int hn = e / DH, d = e % DH;
+    float M = kNegFltMax;
+#pragma unroll
+    for (int ww = 0; ww < RW; ++ww) M = fmaxf(M, mml[(ww * 16 + hn) * 2]);
+    float acc = 0.0f, Ls = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < RW; ++ww) {
+      const float wgt = fast_exp2(mml[(ww * 16 + hn) * 2] - M);
+      acc += wgt * mo[(ww * 16 + hn) * DH + d];
+      Ls += wgt * mml[(ww * 16 + hn) * 2 + 1];
+    }
+    const int64_t row = ((int64_t)b * a.Hq + hk * Gq + hn) * a.splits + split;
+    a.part_o[row * DH + d] = acc;
+    if (d == 0) {
+      a.part_ml[row * 2 + 0] = M;
+      a.part_ml[row * 2 + 1] = Ls;
+    }
+  }
+}
+
 // One work-group per (batch, query head): combine the splits' partials.
 __global__ __launch_bounds__(DH) void decode_combine(const float *part_o,
                                                      const float *part_ml,
@@ -615,7 +832,14 @@ hipError_t launch_decode(const DecodeLaunch &L, hipStream_t s) {
   a.scale2 = L.scale_log2;
   const int grid = (int)(L.batch * L.heads_kv * L.splits);
   if (L.kv_dtype == 3) {
-    hipLaunchKernelGGL(decode_partial<true>, dim3(grid), dim3(DT), 0, s, a);
+    static bool attr8_set = false;  // benign race: the attribute is idempotent
+    if (!attr8_set) {
+      hipError_t e = hipFuncSetAttribute((const void *)decode_partial_ring8,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, R8LDS);
+      if (e != hipSuccess) return e;
+      attr8_set = true;
+    }
+    hipLaunchKernelGGL(decode_partial_ring8, dim3(grid), dim3(RT), R8LDS, s, a);
   } else {
     static bool attr_set = false;  // benign race: the attribute is idempotent
     if (!attr_set) {
