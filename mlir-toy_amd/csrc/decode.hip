@@ -8,28 +8,20 @@
 // exp2 domain:  M = max m_s, w_s = 2^(m_s - M), L = sum w_s l_s,
 // O = sum w_s o~_s / L, lse = (M + log2 L) ln 2.
 //
-// Work decomposition: one 256-thread work-group per (batch, kv head,
-// split); its 4 waves take consecutive quarters of the split, each
-// streaming 32-token steps, and merge through LDS at the end. All query
-// heads of the group (heads_q / heads_kv <= 16) ride in one MFMA tile, so
-// every K/V byte is read from HBM exactly once.
+// Work decomposition: one single-wave work-group per (batch, kv head,
+// split); the wave streams its split in 32-token steps through a private
+// LDS ring filled by global_load_lds_dwordx4 (no K/V byte passes through
+// VGPRs on its way to LDS). All query heads of the group
+// (heads_q / heads_kv <= 16) ride in one MFMA tile, so every K/V byte is
+// read from HBM exactly once. One wave per work-group lets the LDS budget,
+// not the work-group shape, set occupancy (measured fastest).
 //
-// Per 32-token step a wave issues (v_mfma_f32_16x16x32 bf16):
-//   S^T[16 keys x 16 heads]  = K[16 keys x 32 d] . Q^T      (A = K, from
-//                              global straight into VGPRs; 2 x 4 MFMAs)
-//   O^T[16 d x 16 heads]    += V^T[16 d x 32 keys] . P^T    (A = V^T from
-//                              LDS, B = P^T from the S^T accumulators;
-//                              8 MFMAs)
-// V is transposed into a per-wave LDS tile with keys permuted so that the
-// 8 keys a lane contributes to P^T (16x16 accumulator layout: lane group g
-// holds keys 4g..4g+3 and 16+4g..16+4g+3) are contiguous: key 16a+4g+b is
-// stored at position 8g+4a+b. The next step's K/V loads are issued before
-// the current step is consumed.
-//
-// fp8 KV: codes are widened to bf16 in registers (exact), the per-block K
-// scale is folded into the score scale and the V scale into P before its
-// bf16 rounding; 32-token steps never straddle a scale block (the scale
-// block is a multiple of 32 and every wave range starts on a 32 boundary).
+// Per 32-token step (v_mfma_f32_16x16x32_bf16, one lane column per head):
+//   S^T[16 keys x 16 heads]  = K[16 keys x 32 d] . Q^T   (A = K rows, LDS)
+//   O^T[16 d x 16 heads]    += V^T[16 d x 32 keys] . P^T (A = V^T by LDS
+//                              transpose reads, B = P^T from S^T)
+// K/V loads are non-temporal: each byte is used once, and the nt hint
+// measured ~10% more HBM bandwidth for this stream.
 #include "device_common.h"
 #include "kernels.h"
 #include "lds_dma.h"
@@ -37,11 +29,8 @@
 namespace neptune {
 namespace {
 
-constexpr int DT = 256;     // threads per decode work-group
 constexpr int STEP = 32;    // tokens per wave step
 constexpr int DH = 128;     // head_dim covered by the decode kernels
-constexpr int VTP = STEP + 8;      // V^T pitch (elements) for bf16
-constexpr int VTP8 = STEP + 16;    // V^T pitch (bytes) for fp8 codes
 
 struct DecArgs {
   const uint16_t *q;
@@ -52,266 +41,11 @@ struct DecArgs {
   float scale2;
 };
 
-__device__ inline uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
-  return __builtin_amdgcn_perm(hi, lo, sel);
-}
-
 // bf16 bits of 4 E4M3 codes packed in one dword -> two dwords of bf16 pairs
 __device__ inline u32x2 e4m3x4_to_bf16(uint32_t c) {
   f32x2 lo = e4m3x2_to_f32<false>(c);
   f32x2 hi = e4m3x2_to_f32<true>(c);
   return u32x2{Bf16Tag::pack2(lo[0], lo[1]), Bf16Tag::pack2(hi[0], hi[1])};
-}
-
-template <bool FP8>
-__global__ __launch_bounds__(DT, 2) void decode_partial(DecArgs a) {
-  // per-wave V^T tile; reused for the cross-wave merge at the end
-  constexpr int VT_BYTES = FP8 ? DH * VTP8 : DH * VTP * 2;
-  constexpr int MERGE_BYTES = 4 * 16 * DH * 4 + 4 * 16 * 2 * 4;
-  constexpr int SMEM = (4 * VT_BYTES > MERGE_BYTES) ? 4 * VT_BYTES : MERGE_BYTES;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
-
-  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
-  const int n = l & 15, g = l >> 4;  // MFMA column (query head) / lane group
-  const int id = blockIdx.x;
-  const int split = id % a.splits;
-  const int bk = id / a.splits;  // batch * Hk + kv head
-  const int b = bk / a.Hk, hk = bk % a.Hk;
-  const int G = a.group;
-
-  const int c0 = split * a.chunk;
-  const int c1 = min(c0 + a.chunk, a.L);
-  const int wlen = ((a.chunk + 4 * STEP - 1) / (4 * STEP)) * STEP;
-  const int t0 = c0 + w * wlen;
-  const int t1 = min(t0 + wlen, c1);
-
-  // Q^T operand. k-step ks covers head_dim d = dbase(ks, g) + 0..7.
-  u32x4 qf[4];
-  {
-    const uint16_t *qrow = a.q + ((int64_t)b * a.Hq + hk * G + n) * DH;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      int d = FP8 ? 64 * (ks >> 1) + 16 * g + 8 * (ks & 1) : 32 * ks + 8 * g;
-      qf[ks] = n < G ? *(const u32x4 *)(qrow + d) : u32x4{0, 0, 0, 0};
-    }
-  }
-
-  const int64_t kvbase = (int64_t)bk * a.L * DH;  // element (code) offset
-  uint8_t *vt = smem + w * VT_BYTES;
-
-  f32x4 oacc[8];
-#pragma unroll
-  for (int mb = 0; mb < 8; ++mb) oacc[mb] = f32x4{0, 0, 0, 0};
-  float m = kNegFltMax, lsum = 0.0f;
-
-  // register images of one step
-  constexpr int NKR = FP8 ? 4 : 8;  // 16-byte K loads per lane per step
-  constexpr int NVR = FP8 ? 4 : 8;  // 16-byte V loads per lane per step
-  u32x4 kr[NKR], vr[NVR];
-
-  auto load_step = [&](int t) {
-    // K: lane (n16 = l & 15) = key within a 16-key block
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      int key = min(t + 16 * kb + (l & 15), a.L - 1);
-      if (FP8) {
-        const uint8_t *kp = (const uint8_t *)a.k + kvbase + (int64_t)key * DH;
-#pragma unroll
-        for (int sp = 0; sp < 2; ++sp)
-          kr[2 * kb + sp] = __builtin_nontemporal_load((const u32x4 *)(kp + 64 * sp + 16 * g));
-      } else {
-        const uint16_t *kp = (const uint16_t *)a.k + kvbase + (int64_t)key * DH;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-          kr[4 * kb + ks] = *(const u32x4 *)(kp + 32 * ks + 8 * g);
-      }
-    }
-    // V: lane (kq = l >> 3, dc = l & 7) loads tokens 4kq..4kq+3
-    const int kq = l >> 3, dc = l & 7;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      int key = min(t + 4 * kq + i, a.L - 1);
-      if (FP8) {
-        const uint8_t *vp = (const uint8_t *)a.v + kvbase + (int64_t)key * DH;
-        vr[i] = __builtin_nontemporal_load((const u32x4 *)(vp + 16 * dc));
-      } else {
-        const uint16_t *vp = (const uint16_t *)a.v + kvbase + (int64_t)key * DH;
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
-          vr[2 * i + hh] = *(const u32x4 *)(vp + 64 * hh + 8 * dc);
-      }
-    }
-  };
-
-  if (t0 < t1) load_step(t0);
-  for (int t = t0; t < t1; t += STEP) {
-    u32x4 kc[NKR], vc[NVR];
-#pragma unroll
-    for (int i = 0; i < NKR; ++i) kc[i] = kr[i];
-#pragma unroll
-    for (int i = 0; i < NVR; ++i) vc[i] = vr[i];
-    if (t + STEP < t1) load_step(t + STEP);
-
-    // ---- S^T = K Q^T
-    f32x4 s[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      s[kb] = f32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        u32x4 A;
-        if (FP8) {
-          u32x4 c = kc[2 * kb + (ks >> 1)];
-          u32x2 lo = e4m3x4_to_bf16(c[2 * (ks & 1)]);
-          u32x2 hi = e4m3x4_to_bf16(c[2 * (ks & 1) + 1]);
-          A = u32x4{lo[0], lo[1], hi[0], hi[1]};
-        } else {
-          A = kc[4 * kb + ks];
-        }
-        s[kb] = Bf16Tag::mfma16(as_vec8<bf16x8>(A), as_vec8<bf16x8>(qf[ks]), s[kb]);
-      }
-    }
-    float sc = a.scale2, vsc = 1.0f;
-    if (FP8) {
-      const int blk = t / a.sb;
-      sc *= a.ksc[(int64_t)bk * a.nsb + blk];
-      vsc = a.vsc[(int64_t)bk * a.nsb + blk];
-    }
-    // scale first, then mask: a zero fp8 scale must not meet -inf
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s[kb][r] *= sc;
-    if (t + STEP > t1) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (t + 16 * kb + 4 * g + r >= t1) s[kb][r] = -INFINITY;
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kb][r]);
-    mx = wave_max_xor(mx, 16);
-    mx = wave_max_xor(mx, 32);
-    const float m_new = fmaxf(m, mx);
-    const float alpha = fast_exp2(m - m_new);
-    float rs = 0.0f;
-    float p[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float e = fast_exp2(s[j >> 2][j & 3] - m_new);
-      rs += e;
-      p[j] = e;
-    }
-    lsum = lsum * alpha + rs;
-    m = m_new;
-    if (__any(alpha != 1.0f)) {
-#pragma unroll
-      for (int mb = 0; mb < 8; ++mb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) oacc[mb][r] *= alpha;
-    }
-    u32x4 pf;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      pf[i] = FP8 ? Bf16Tag::pack2(p[2 * i] * vsc, p[2 * i + 1] * vsc)
-                  : Bf16Tag::pack2(p[2 * i], p[2 * i + 1]);
-
-    // ---- V^T into this wave's LDS tile
-    {
-      const int kq = l >> 3, dc = l & 7;
-      const int pos = 8 * (kq & 3) + 4 * (kq >> 2);
-      if (FP8) {
-#pragma unroll
-        for (int dg = 0; dg < 4; ++dg) {
-          uint32_t w0 = vc[0][dg], w1 = vc[1][dg], w2 = vc[2][dg], w3 = vc[3][dg];
-          uint32_t t0_ = perm_b32(w1, w0, 0x05010400u);
-          uint32_t t1_ = perm_b32(w1, w0, 0x07030602u);
-          uint32_t t2_ = perm_b32(w3, w2, 0x05010400u);
-          uint32_t t3_ = perm_b32(w3, w2, 0x07030602u);
-          uint32_t o4[4] = {perm_b32(t2_, t0_, 0x05040100u), perm_b32(t2_, t0_, 0x07060302u),
-                            perm_b32(t3_, t1_, 0x05040100u), perm_b32(t3_, t1_, 0x07060302u)};
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            *(uint32_t *)(vt + (16 * dc + 4 * dg + e) * VTP8 + pos) = o4[e];
-        }
-      } else {
-        uint16_t *vt16 = (uint16_t *)vt;
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-            u32x2 val = {perm_b32(vc[2 * 1 + hh][e >> 1], vc[2 * 0 + hh][e >> 1], sel),
-                         perm_b32(vc[2 * 3 + hh][e >> 1], vc[2 * 2 + hh][e >> 1], sel)};
-            *(u32x2 *)(vt16 + (64 * hh + 8 * dc + e) * VTP + pos) = val;
-          }
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    // ---- O^T += V^T P^T
-#pragma unroll
-    for (int mb = 0; mb < 8; ++mb) {
-      u32x4 A;
-      if (FP8) {
-        u32x2 c = *(const u32x2 *)(vt + (16 * mb + n) * VTP8 + 8 * g);
-        u32x2 lo = e4m3x4_to_bf16(c[0]);
-        u32x2 hi = e4m3x4_to_bf16(c[1]);
-        A = u32x4{lo[0], lo[1], hi[0], hi[1]};
-      } else {
-        A = *(const u32x4 *)((const uint16_t *)vt + (16 * mb + n) * VTP + 8 * g);
-      }
-      oacc[mb] = Bf16Tag::mfma16(as_vec8<bf16x8>(A), as_vec8<bf16x8>(pf), oacc[mb]);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  }
-
-  // per-head row sum across the four lane groups
-  lsum += __shfl_xor(lsum, 16, 64);
-  lsum += __shfl_xor(lsum, 32, 64);
-
-  // ---- merge the four waves of this split
-  __syncthreads();
-  float *mo = (float *)smem;              // [4][16][DH]
-  float *mml = mo + 4 * 16 * DH;          // [4][16][2]
-  if (n < G) {
-#pragma unroll
-    for (int mb = 0; mb < 8; ++mb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) mo[(w * 16 + n) * DH + 16 * mb + 4 * g + r] = oacc[mb][r];
-    if (g == 0) {
-      mml[(w * 16 + n) * 2 + 0] = m;
-      mml[(w * 16 + n) * 2 + 1] = lsum;
-    }
-  }
-  __syncthreads();
-  for (int e = tid; e < G * DH; e += DT) {
-    const int hn = e / DH, d = e % DH;
-    float M = kNegFltMax;
-#pragma unroll
-    for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, mml[(ww * 16 + hn) * 2]);
-    float acc = 0.0f, Ls = 0.0f;
-#pragma unroll
-    for (int ww = 0; ww < 4; ++ww) {
-      float wgt = fast_exp2(mml[(ww * 16 + hn) * 2] - M);
-      acc += wgt * mo[(ww * 16 + hn) * DH + d];
-      Ls += wgt * mml[(ww * 16 + hn) * 2 + 1];
-    }
-    const int64_t row = ((int64_t)b * a.Hq + hk * G + hn) * a.splits + split;
-    a.part_o[row * DH + d] = acc;
-    if (d == 0) {
-      a.part_ml[row * 2 + 0] = M;
-      a.part_ml[row * 2 + 1] = Ls;
-    }
-  }
 }
 
 // bf16 KV through LDS: each wave streams its token range in 32-token steps
@@ -328,9 +62,9 @@ constexpr int RSTEP = 32;                   // tokens per step
 constexpr int RTILE = RSTEP * DH * 2;       // bytes of one K or V tile
 constexpr int RSLOT = 2 * RTILE;            // K + V
 constexpr int RWAVE = 2 * RSLOT;            // two slots per wave
-constexpr int RW = 2;                       // waves per work-group
+constexpr int RW = 1;                       // waves per work-group (LDS-bound occupancy)
 constexpr int RT = 64 * RW;                 // threads per work-group
-constexpr int RLDS = RW * RWAVE;            // two work-groups fit one CU
+constexpr int RLDS = RW * RWAVE;
 
 __global__ __launch_bounds__(RT) void decode_partial_ring(DecArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -538,15 +272,18 @@ __global__ __launch_bounds__(RT) void decode_partial_ring(DecArgs a) {
 //   V tile: same layout; V^T comes from ds_read_b64_tr_b8, whose source
 //           lane pair (2i, 2i+1) names the token row of k-slot i, so the
 //           rows can follow the P^T key order directly.
+constexpr int R8W = 1;                      // waves per work-group (LDS-bound occupancy)
+constexpr int R8T = 64 * R8W;
 constexpr int R8TILE = RSTEP * DH;          // bytes of one K or V code tile
 constexpr int R8SLOT = 2 * R8TILE;
-constexpr int R8WAVE = 2 * R8SLOT;
-constexpr int R8LDS = RW * R8WAVE;
+constexpr int R8NS = 2;                     // ring slots: 1 step in flight
+constexpr int R8WAVE = R8NS * R8SLOT;
+constexpr int R8LDS = R8W * R8WAVE;
 
 typedef int v2i32 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) v2i32 lds_v2i32;
 
-__global__ __launch_bounds__(RT) void decode_partial_ring8(DecArgs a) {
+__global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -559,7 +296,7 @@ __global__ __launch_bounds__(RT) void decode_partial_ring8(DecArgs a) {
 
   const int c0 = split * a.chunk;
   const int c1 = min(c0 + a.chunk, a.L);
-  const int wlen = ((a.chunk + RW * RSTEP - 1) / (RW * RSTEP)) * RSTEP;
+  const int wlen = ((a.chunk + R8W * RSTEP - 1) / (R8W * RSTEP)) * RSTEP;
   const int t0 = c0 + w * wlen;
   const int t1 = min(t0 + wlen, c1);
   const int nsteps = t1 > t0 ? (t1 - t0 + RSTEP - 1) / RSTEP : 0;
@@ -577,7 +314,7 @@ __global__ __launch_bounds__(RT) void decode_partial_ring8(DecArgs a) {
   }
   auto issue = [&](int i) {
     const int tb = t0 + i * RSTEP;
-    const uint8_t *slot = ring + (i & 1) * R8SLOT;
+    const uint8_t *slot = ring + (i % R8NS) * R8SLOT;
     if (tb + RSTEP <= a.L) {
       const char *kb = kbase + (int64_t)tb * DH, *vb = vbase + (int64_t)tb * DH;
 #pragma unroll
@@ -595,8 +332,9 @@ __global__ __launch_bounds__(RT) void decode_partial_ring8(DecArgs a) {
       }
     }
   };
-  if (nsteps > 0) issue(0);
-  if (nsteps > 1) issue(1);
+#pragma unroll
+  for (int i = 0; i < R8NS - 1; ++i)
+    if (i < nsteps) issue(i);
 
   // Q^T operand: k-step ks covers head_dim 64 (ks >> 1) + 16 G + 8 (ks & 1) .. +7
   u32x4 qf[4];
@@ -625,11 +363,16 @@ __global__ __launch_bounds__(RT) void decode_partial_ring8(DecArgs a) {
   float m = kNegFltMax, lsum = 0.0f;
 
   for (int i = 0; i < nsteps; ++i) {
-    if (i + 1 < nsteps)
+    // this step's 8 copies have landed once only the later steps' may be
+    // outstanding
+    const int later = min(R8NS - 2, nsteps - 1 - i);
+    if (later >= 2)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(16));
+    else if (later == 1)
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(8));
     else
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-    const uint8_t *kt = ring + (i & 1) * R8SLOT;
+    const uint8_t *kt = ring + (i % R8NS) * R8SLOT;
     const uint8_t *vt = kt + R8TILE;
     const int t = t0 + i * RSTEP;
 
@@ -702,15 +445,15 @@ __global__ __launch_bounds__(RT) void decode_partial_ring8(DecArgs a) {
       oacc[mb] = Bf16Tag::mfma16(as_vec8<bf16x8>(A), as_vec8<bf16x8>(pf), oacc[mb]);
     }
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-    if (i + 2 < nsteps) issue(i + 2);
+    if (i + R8NS - 1 < nsteps) issue(i + R8NS - 1);
   }
 
   lsum += __shfl_xor(lsum, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);
 
   __syncthreads();
-  float *mo = (float *)smem;              // [RW][16][DH]
-  float *mml = mo + RW * 16 * DH;         // [RW][16][2]
+  float *mo = (float *)smem;              // [R8W][16][DH]
+  float *mml = mo + R8W * 16 * DH;         // [R8W][16][2]
   if (n < Gq) {
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb)
@@ -722,14 +465,14 @@ __global__ __launch_bounds__(RT) void decode_partial_ring8(DecArgs a) {
     }
   }
   __syncthreads();
-  for (int e = tid; e < Gq * DH; e += RT) {
+  for (int e = tid; e < Gq * DH; e += R8T) {
     const int hn = e / DH, d = e % DH;
     float M = kNegFltMax;
 #pragma unroll
-    for (int ww = 0; ww < RW; ++ww) M = fmaxf(M, mml[(ww * 16 + hn) * 2]);
+    for (int ww = 0; ww < R8W; ++ww) M = fmaxf(M, mml[(ww * 16 + hn) * 2]);
     float acc = 0.0f, Ls = 0.0f;
 #pragma unroll
-    for (int ww = 0; ww < RW; ++ww) {
+    for (int ww = 0; ww < R8W; ++ww) {
       const float wgt = fast_exp2(mml[(ww * 16 + hn) * 2] - M);
       acc += wgt * mo[(ww * 16 + hn) * DH + d];
       Ls += wgt * mml[(ww * 16 + hn) * 2 + 1];
@@ -744,23 +487,45 @@ __global__ __launch_bounds__(RT) void decode_partial_ring8(DecArgs a) {
 }
 
 // One work-group per (batch, query head): combine the splits' partials.
+// Wave 0 reads every split's (m, l) at once (one lane per split), reduces
+// M and L across the wave and leaves the weights 2^(m_s - M) in LDS; then
+// every thread (one head_dim element) sums its splits' o~ with the loads
+// unrolled so they are in flight together.
 __global__ __launch_bounds__(DH) void decode_combine(const float *part_o,
                                                      const float *part_ml,
                                                      uint16_t *o, float *lse,
                                                      int32_t splits) {
+  extern __shared__ float wts[];  // [splits]
+  __shared__ float stat[2];
   const int64_t bh = blockIdx.x;
   const int d = threadIdx.x;
   const float *ml = part_ml + bh * splits * 2;
-  float M = kNegFltMax;
-  for (int s = 0; s < splits; ++s) M = fmaxf(M, ml[2 * s]);
-  float Ls = 0.0f, acc = 0.0f;
-  for (int s = 0; s < splits; ++s) {
-    float wgt = fast_exp2(ml[2 * s] - M);
-    Ls += wgt * ml[2 * s + 1];
-    acc += wgt * part_o[(bh * splits + s) * DH + d];
+  if (d < 64) {
+    float M = kNegFltMax;
+    for (int s = d; s < splits; s += 64) M = fmaxf(M, ml[2 * s]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    float Ls = 0.0f;
+    for (int s = d; s < splits; s += 64) {
+      const float wgt = fast_exp2(ml[2 * s] - M);
+      wts[s] = wgt;
+      Ls += wgt * ml[2 * s + 1];
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) Ls += __shfl_xor(Ls, off, 64);
+    if (d == 0) {
+      stat[0] = M;
+      stat[1] = Ls;
+    }
   }
+  __syncthreads();
+  const float *po = part_o + bh * splits * DH + d;
+  float acc = 0.0f;
+#pragma unroll 8
+  for (int s = 0; s < splits; ++s) acc += wts[s] * po[(int64_t)s * DH];
+  const float Ls = stat[1];
   o[bh * DH + d] = Bf16Tag::from_f32(acc / Ls);
-  if (d == 0 && lse) lse[bh] = (M + log2f(Ls)) * kLn2;
+  if (d == 0 && lse) lse[bh] = (stat[0] + log2f(Ls)) * kLn2;
 }
 
 // One work-group per (batch, kv head, scale block): amax, scale, codes.
@@ -839,7 +604,7 @@ hipError_t launch_decode(const DecodeLaunch &L, hipStream_t s) {
       if (e != hipSuccess) return e;
       attr8_set = true;
     }
-    hipLaunchKernelGGL(decode_partial_ring8, dim3(grid), dim3(RT), R8LDS, s, a);
+    hipLaunchKernelGGL(decode_partial_ring8, dim3(grid), dim3(R8T), R8LDS, s, a);
   } else {
     static bool attr_set = false;  // benign race: the attribute is idempotent
     if (!attr_set) {
@@ -852,7 +617,8 @@ hipError_t launch_decode(const DecodeLaunch &L, hipStream_t s) {
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(decode_combine, dim3((unsigned)(L.batch * L.heads_q)), dim3(DH), 0, s,
+  hipLaunchKernelGGL(decode_combine, dim3((unsigned)(L.batch * L.heads_q)), dim3(DH),
+                     (size_t)L.splits * sizeof(float), s,
                      (const float *)L.part_o, (const float *)L.part_ml, (uint16_t *)L.o,
                      L.lse, (int32_t)L.splits);
   return hipGetLastError();
