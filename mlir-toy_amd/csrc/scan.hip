@@ -7,20 +7,34 @@
 //   x_n  <- 2^(delta * A[d,n] * log2 e) x_n + (delta u) B[b,n,l]
 //   y     = (sum_n C[b,n,l] x_n + D[d] u) * silu(z)
 //
-// Mapping: a channel (batch b, inner dim d) is owned by NL adjacent lanes,
-// each carrying 16/NL of its fp32 states in registers and walking the
-// sequence in order, so no carry ever crosses lanes or work-groups. The
-// per-step output reduction over states is an in-row DPP butterfly
-// (quad_perm xor1/xor2, row_half_mirror, row_mirror). A 256-thread
-// work-group owns 256/NL channels of one batch row and stages 64-step tiles
-// through LDS: the channel rows of u / delta_raw / z arrive as coalesced
-// 16-byte loads, the per-(channel, step) terms (delta, delta*u, D*u,
-// silu(z)) are computed once per tile by the whole group, B and C (shared by
-// every channel of the batch row) are read once per tile, and y leaves
-// through an LDS tile as coalesced 16-byte stores.
+// The per-state update (one exp2, two multiplies, one FMA, one multiply for
+// the output term) is VALU/transcendental work: 16 states per (channel,
+// step) against 8 bytes of HBM traffic, so the kernel is bound by the VALU,
+// not by HBM. The design therefore maximises the number of independent
+// wavefronts per SIMD and keeps every other cost off the VALU:
 //
-// The per-state update (one exp2, one mul, two FMAs) is VALU/transcendental
-// work that no layout removes; the kernel is compute-bound, not HBM-bound.
+// Mapping: a 256-thread work-group owns 16 channels of one batch row; lane
+// (wave w, row r = lane / 16, column c = lane % 16) carries the single fp32
+// state n = 4 w + r of channel c and walks the sequence in order, so no
+// carry crosses lanes. 16-channel work-groups give every CU the same share
+// of channels (batch * dim / 16 groups), and one state per lane gives four
+// or five resident wavefronts per SIMD to hide the exp2 -> FMA chain.
+//
+// Per 32-step chunk:
+//   stage  each thread loads 2 steps of u / delta_raw / z of one channel
+//          (64-byte row segments per wave) and B / C of one state, computes
+//          (delta, delta*u) and (B, C) into LDS, and keeps (D*u, silu(z))
+//          in registers for its own outputs; the next chunk's loads are
+//          issued before the recurrence so their latency is hidden.
+//   scan   lanes read (delta, delta*u) of their channel and (B, C) of their
+//          state with 16-byte LDS reads covering two steps (broadcast
+//          across the lanes that share them) and keep C_n x_n per step.
+//   reduce the 16-state sum is a transposed butterfly: v_permlane32_swap
+//          then v_permlane16_swap each exchange one register pair and add,
+//          leaving every lane with the 4-state sum of 8 of the 32 steps;
+//          the four waves' sums meet in LDS.
+//   store  each thread adds the four wave sums for its two steps, applies
+//          D*u and the gate and stores two bf16 outputs.
 #include "device_common.h"
 #include "kernels.h"
 
@@ -28,175 +42,196 @@ namespace neptune {
 namespace {
 
 constexpr int ST = 16;     // d_state covered
-constexpr int TT = 64;     // steps per LDS tile
+constexpr int SCH = 16;    // channels per work-group
+constexpr int TT = 32;     // steps per chunk
 constexpr int NT = 256;    // threads per work-group
+constexpr int TP = TT / 2; // step pairs per chunk
 
 struct ScanArgs {
   const uint16_t *u, *dr, *Bm, *Cm, *z;
   const float *A, *D, *bias;
   uint16_t *y;
   int32_t Dm, L, softplus;
-  int32_t vec;  // rows are 16-byte aligned: L % 8 == 0 and aligned bases
+  int32_t vec;  // 4-byte pair access: L even and every base 4-byte aligned
 };
 
-template <int CTRL>
-__device__ inline float dpp(float x) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, true));
+__device__ inline float lo_bf16(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ inline float hi_bf16(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
+
+// two consecutive bf16 elements of a row as packed bits; t is even and
+// elements at or beyond L read as zero
+__device__ inline uint32_t load_pair(const uint16_t *row, int t, int L, bool vec) {
+  if (vec && t + 1 < L) return *(const uint32_t *)(row + t);
+  uint32_t lo = t < L ? row[t] : 0u;
+  uint32_t hi = t + 1 < L ? row[t + 1] : 0u;
+  return lo | (hi << 16);
 }
 
-// sum over NL adjacent lanes (NL in 1,2,4,8,16), result in every lane
-template <int NL>
-__device__ inline float group_sum(float x) {
-  if (NL >= 2) x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
-  if (NL >= 4) x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
-  if (NL >= 8) x += dpp<0x141>(x);  // row_half_mirror
-  if (NL >= 16) x += dpp<0x140>(x); // row_mirror
-  return x;
+__device__ inline float softplus_fast(float v) {
+  // log(1 + e^v) = ln2 * log2(1 + 2^(v log2 e)); torch returns v above 20
+  return v > 20.0f ? v : 0.69314718055994531f * __builtin_amdgcn_logf(1.0f + fast_exp2(v * kLog2e));
 }
 
-template <int NL>
+__device__ inline float silu_fast(float z) {
+  return z * __builtin_amdgcn_rcpf(1.0f + fast_exp2(-z * kLog2e));
+}
+
+// (lane, lane ^ 32) exchange: returns a_lo + a_hi in the low half and
+// b_lo + b_hi in the high half
+__device__ inline float fold32(float a, float b) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// row pairs (0,1) and (2,3): returns a summed over the pair in even rows
+// and b summed over the pair in odd rows
+__device__ inline float fold16(float a, float b) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __global__ __launch_bounds__(NT) void selective_scan_fwd(ScanArgs a) {
-  constexpr int SPL = ST / NL;     // states per lane
-  constexpr int CPB = NT / NL;     // channels per work-group
-  constexpr int CPR = TT / 8;      // 16-byte chunks per channel row of a tile
-  // rows padded by one element so lanes of different channels / states
-  // land in different LDS banks
-  __shared__ __attribute__((aligned(16))) float2 pre[CPB][TT + 1];   // (delta, delta*u)
-  __shared__ __attribute__((aligned(16))) float2 post[CPB][TT + 1];  // (D*u, silu(z))
-  __shared__ __attribute__((aligned(16))) float bc[2][ST][TT + 1];   // B, C
-  __shared__ __attribute__((aligned(16))) float yt[CPB][TT + 1];
+  // (delta, delta*u) and (B, C) for two steps per float4; one float4 of
+  // padding per row keeps the 16 rows read together in distinct banks
+  __shared__ float4 pre[SCH][TP + 1];
+  __shared__ float4 bcs[ST][TP + 1];
+  // per-wave 4-state sums, [wave][step][channel], padded rows
+  __shared__ float part[4][TT][SCH + 1];
 
-  const int tid = threadIdx.x;
-  const int nblk = (a.Dm + CPB - 1) / CPB;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = tid >> 6;
+  const int nblk = (a.Dm + SCH - 1) / SCH;
   const int b = blockIdx.x / nblk;
-  const int d0 = (blockIdx.x % nblk) * CPB;
+  const int d0 = (blockIdx.x % nblk) * SCH;
 
-  // compute-phase identity
-  const int cw = tid / NL;        // channel within the group
-  const int j = tid % NL;         // state slice
-  const int dch = d0 + cw;
-  float A2[SPL], x[SPL];
-#pragma unroll
-  for (int s = 0; s < SPL; ++s) {
-    A2[s] = dch < a.Dm ? a.A[(int64_t)dch * ST + j * SPL + s] * kLog2e : 0.0f;
-    x[s] = 0.0f;
-  }
+  // scan identity: channel c, state n
+  const int c = lane & 15, r = lane >> 4;
+  const int n = 4 * w + r;
+  const bool cok = d0 + c < a.Dm;
+  const float A2 = cok ? a.A[(int64_t)(d0 + c) * ST + n] * kLog2e : 0.0f;
+  float x = 0.0f;
 
-  const int64_t rowbase = ((int64_t)b * a.Dm) * a.L;
-  const int64_t bcbase = (int64_t)b * ST * a.L;
+  // stage / store identity: channel sc, steps 2 sp and 2 sp + 1 of a chunk;
+  // B / C identity: state tid / 16, same step pair
+  const int sc = tid / TP, sp = tid % TP;
+  const int sd = d0 + sc;
+  const bool sok = sd < a.Dm;
+  const int bn = tid / TP;
+  const int64_t srow = ((int64_t)b * a.Dm + (sok ? sd : 0)) * a.L;
+  const int64_t bcrow = ((int64_t)b * ST + bn) * a.L;
+  const float bias = (sok && a.bias) ? a.bias[sd] : 0.0f;
+  const float Dd = (sok && a.D) ? a.D[sd] : 0.0f;
+  const bool vec = a.vec != 0;
 
+  // the reduced sums a lane holds after the butterfly are for steps
+  // 4 m + rs, m = 0..7, with rs = 2 (r & 1) + (r >> 1)
+  const int rs = 2 * (r & 1) + (r >> 1);
+
+  uint32_t pu = 0, pdr = 0, pz = 0, pB = 0, pC = 0;
+  auto fetch = [&](int t0) {
+    const int t = t0 + 2 * sp;
+    if (vec && t0 + TT <= a.L) {  // whole chunk in range: one dword per row
+      if (sok) {
+        pu = *(const uint32_t *)(a.u + srow + t);
+        pdr = *(const uint32_t *)(a.dr + srow + t);
+        if (a.z) pz = *(const uint32_t *)(a.z + srow + t);
+      }
+      pB = *(const uint32_t *)(a.Bm + bcrow + t);
+      pC = *(const uint32_t *)(a.Cm + bcrow + t);
+    } else {
+      if (sok) {
+        pu = load_pair(a.u + srow, t, a.L, vec);
+        pdr = load_pair(a.dr + srow, t, a.L, vec);
+        pz = a.z ? load_pair(a.z + srow, t, a.L, vec) : 0u;
+      }
+      pB = load_pair(a.Bm + bcrow, t, a.L, vec);
+      pC = load_pair(a.Cm + bcrow, t, a.L, vec);
+    }
+  };
+
+  fetch(0);
   for (int t0 = 0; t0 < a.L; t0 += TT) {
-    const int tn = min(TT, a.L - t0);
-    // ---- stage: per-(channel, step) terms
-    for (int c = tid; c < CPB * CPR; c += NT) {
-      const int ch = c / CPR, k8 = c % CPR, dd = d0 + ch;
-      const int tt = 8 * k8;
-      float uu[8], dl[8], zz[8];
-      if (a.vec && dd < a.Dm && t0 + tt + 8 <= a.L) {
-        const int64_t off = rowbase + (int64_t)dd * a.L + t0 + tt;
-        u32x4 uv = *(const u32x4 *)(a.u + off);
-        u32x4 dv = *(const u32x4 *)(a.dr + off);
-        u32x4 zv = a.z ? *(const u32x4 *)(a.z + off) : u32x4{0, 0, 0, 0};
+    // ---- stage
+    float du2[2], gate[2];
+    {
+      const float uu[2] = {lo_bf16(pu), hi_bf16(pu)};
+      const float dl[2] = {lo_bf16(pdr), hi_bf16(pdr)};
+      const float zz[2] = {lo_bf16(pz), hi_bf16(pz)};
+      float4 pv;
+      float *pf = reinterpret_cast<float *>(&pv);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          uu[2 * i] = __uint_as_float(uv[i] << 16);
-          uu[2 * i + 1] = __uint_as_float(uv[i] & 0xffff0000u);
-          dl[2 * i] = __uint_as_float(dv[i] << 16);
-          dl[2 * i + 1] = __uint_as_float(dv[i] & 0xffff0000u);
-          zz[2 * i] = __uint_as_float(zv[i] << 16);
-          zz[2 * i + 1] = __uint_as_float(zv[i] & 0xffff0000u);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          bool ok = dd < a.Dm && t0 + tt + i < a.L;
-          int64_t off = rowbase + (int64_t)dd * a.L + t0 + tt + i;
-          uu[i] = ok ? Bf16Tag::to_f32(a.u[off]) : 0.0f;
-          dl[i] = ok ? Bf16Tag::to_f32(a.dr[off]) : 0.0f;
-          zz[i] = ok && a.z ? Bf16Tag::to_f32(a.z[off]) : 0.0f;
-        }
+      for (int i = 0; i < 2; ++i) {
+        const float v = dl[i] + bias;
+        // steps past the end carry delta = 0 and delta*u = 0 (x unchanged)
+        const bool in = t0 + 2 * sp + i < a.L;
+        const float delta = in ? (a.softplus ? softplus_fast(v) : v) : 0.0f;
+        pf[2 * i] = delta;
+        pf[2 * i + 1] = delta * uu[i];
+        du2[i] = Dd * uu[i];
+        gate[i] = a.z ? silu_fast(zz[i]) : 1.0f;
       }
-      const float bias = (dd < a.Dm && a.bias) ? a.bias[dd] : 0.0f;
-      const float Dd = (dd < a.Dm && a.D) ? a.D[dd] : 0.0f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float v = dl[i] + bias;
-        float delta = a.softplus ? (v > 20.0f ? v : log1pf(__expf(v))) : v;
-        float gate = a.z ? zz[i] / (1.0f + __expf(-zz[i])) : 1.0f;
-        pre[ch][tt + i] = make_float2(delta, delta * uu[i]);
-        post[ch][tt + i] = make_float2(Dd * uu[i], gate);
-      }
+      pre[sc][sp] = pv;
+      bcs[bn][sp] = make_float4(lo_bf16(pB), lo_bf16(pC), hi_bf16(pB), hi_bf16(pC));
     }
-    for (int c = tid; c < 2 * ST * CPR; c += NT) {
-      const int which = c / (ST * CPR), r = (c / CPR) % ST, tt = 8 * (c % CPR);
-      const uint16_t *src = which ? a.Cm : a.Bm;
-      const int64_t off = bcbase + (int64_t)r * a.L + t0 + tt;
-      if (a.vec && t0 + tt + 8 <= a.L) {
-        u32x4 v = *(const u32x4 *)(src + off);
+    if (t0 + TT < a.L) fetch(t0 + TT);
+    __syncthreads();
+
+    // ---- scan: C_n x_n per step
+    float p[TT];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          bc[which][r][tt + 2 * i] = __uint_as_float(v[i] << 16);
-          bc[which][r][tt + 2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
-        }
-      } else {
+    for (int j = 0; j < TP; ++j) {
+      const float4 pd = pre[c][j];
+      const float4 q = bcs[n][j];
+      x = fmaf(fast_exp2(pd.x * A2), x, pd.y * q.x);
+      p[2 * j] = q.y * x;
+      x = fmaf(fast_exp2(pd.z * A2), x, pd.w * q.z);
+      p[2 * j + 1] = q.w * x;
+    }
+    // ---- reduce over the wave's 4 states (rows): after fold32 lane half h
+    // holds steps 2 k + h, after fold16 row r holds steps 4 m + rs
+    float h1[TP];
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-          bc[which][r][tt + i] = t0 + tt + i < a.L ? Bf16Tag::to_f32(src[off + i]) : 0.0f;
-      }
+    for (int k = 0; k < TP; ++k) h1[k] = fold32(p[2 * k], p[2 * k + 1]);
+#pragma unroll
+    for (int m = 0; m < TT / 4; ++m) {
+      const float s = fold16(h1[2 * m], h1[2 * m + 1]);
+      part[w][4 * m + rs][c] = s;
     }
     __syncthreads();
 
-    // ---- recurrence over the tile
-    for (int t = 0; t < tn; ++t) {
-      const float2 pd = pre[cw][t];
-      float acc = 0.0f;
+    // ---- store
+    if (sok) {
+      float yv[2];
 #pragma unroll
-      for (int s = 0; s < SPL; ++s) {
-        const int nn = j * SPL + s;
-        const float da = fast_exp2(pd.x * A2[s]);
-        x[s] = fmaf(da, x[s], pd.y * bc[0][nn][t]);
-        acc = fmaf(bc[1][nn][t], x[s], acc);
+      for (int i = 0; i < 2; ++i) {
+        const int t = 2 * sp + i;
+        const float acc = part[0][t][sc] + part[1][t][sc] + part[2][t][sc] + part[3][t][sc];
+        yv[i] = (acc + du2[i]) * gate[i];
       }
-      acc = group_sum<NL>(acc);
-      if (j == 0) {
-        const float2 po = post[cw][t];
-        yt[cw][t] = (acc + po.x) * po.y;
-      }
-    }
-    __syncthreads();
-
-    // ---- y tile out (bf16, coalesced)
-    for (int c = tid; c < CPB * CPR; c += NT) {
-      const int ch = c / CPR, tt = 8 * (c % CPR), dd = d0 + ch;
-      if (dd >= a.Dm) continue;
-      const int64_t off = rowbase + (int64_t)dd * a.L + t0 + tt;
-      if (a.vec && t0 + tt + 8 <= a.L) {
-        u32x4 v;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          v[i] = Bf16Tag::pack2(yt[ch][tt + 2 * i], yt[ch][tt + 2 * i + 1]);
-        *(u32x4 *)(a.y + off) = v;
+      const int t = t0 + 2 * sp;
+      uint16_t *yrow = a.y + srow;
+      if (vec && t + 1 < a.L) {
+        *(uint32_t *)(yrow + t) = Bf16Tag::pack2(yv[0], yv[1]);
       } else {
-        for (int i = 0; i < 8 && t0 + tt + i < a.L; ++i)
-          a.y[off + i] = Bf16Tag::from_f32(yt[ch][tt + i]);
+        if (t < a.L) yrow[t] = Bf16Tag::from_f32(yv[0]);
+        if (t + 1 < a.L) yrow[t + 1] = Bf16Tag::from_f32(yv[1]);
       }
     }
-    // the next tile's staging writes pre/post/bc only after every wave has
-    // finished reading them
-    __syncthreads();
+    // pre / bcs are rewritten by the next stage only after every wave has
+    // passed this chunk's second barrier, and part only after the next
+    // chunk's first barrier, which every wave reaches after its stores
   }
 }
 
 }  // namespace
-
-constexpr int kScanLanes = 8;
 
 bool scan_supported(const ScanLaunch &a, const char **why) {
   if (a.d_state != ST) {
     *why = "selective scan supports d_state 16";
     return false;
   }
-  if (a.seq_len > (int64_t)1 << 30 || a.dim > (int64_t)1 << 30 || a.batch > 65535) {
+  if (a.seq_len > (int64_t)1 << 30 || a.dim > (int64_t)1 << 30 ||
+      a.batch * ((a.dim + SCH - 1) / SCH) > (((int64_t)1 << 31) - 1)) {
     *why = "selective scan shape too large for one launch";
     return false;
   }
@@ -217,13 +252,11 @@ hipError_t launch_selective_scan(const ScanLaunch &L, hipStream_t s) {
   a.Dm = (int32_t)L.dim;
   a.L = (int32_t)L.seq_len;
   a.softplus = L.delta_softplus;
-  auto al16 = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
-  a.vec = (L.seq_len % 8 == 0) && al16(L.u) && al16(L.delta_raw) && al16(L.B) &&
-          al16(L.C) && al16(L.y) && (!L.z || al16(L.z));
-  constexpr int CPB = NT / kScanLanes;
-  const int nblk = (int)((L.dim + CPB - 1) / CPB);
-  hipLaunchKernelGGL(selective_scan_fwd<kScanLanes>, dim3((unsigned)(nblk * L.batch)), dim3(NT), 0,
-                     s, a);
+  auto al4 = [](const void *p) { return ((uintptr_t)p & 3u) == 0; };
+  a.vec = (L.seq_len % 2 == 0) && al4(L.u) && al4(L.delta_raw) && al4(L.B) && al4(L.C) &&
+          al4(L.y) && (!L.z || al4(L.z));
+  const int64_t nblk = (L.dim + SCH - 1) / SCH;
+  hipLaunchKernelGGL(selective_scan_fwd, dim3((unsigned)(nblk * L.batch)), dim3(NT), 0, s, a);
   return hipGetLastError();
 }
 
