@@ -529,6 +529,67 @@ __global__ __launch_bounds__(DH) void decode_combine(const float *part_o,
 }
 
 // One work-group per (batch, kv head, scale block): amax, scale, codes.
+// fp8 KV quantiser, register path: one 256-thread work-group per (batch,
+// kv head, scale block) whose block holds at most 256 * QMAX chunks of 8
+// elements. The block is read once with non-temporal 16-byte loads into
+// registers, reduced to amax, scaled and converted from registers, so HBM
+// sees one read of the bf16 source and one write of the codes.
+// v_cvt_pk_fp8_f32 is the OCP E4M3 conversion with round to nearest even;
+// scaled magnitudes exceed 448 by at most the rounding of 448 / amax, which
+// rounds back to 448, so the saturating case of the format never arises.
+constexpr int QMAX = 8;
+
+template <int NC>
+__global__ __launch_bounds__(256) void kv_quantize_reg(const uint16_t *src, uint8_t *codes,
+                                                       float *scales, int32_t L, int32_t D,
+                                                       int32_t sb, int32_t nsb) {
+  __shared__ float red[4];
+  const int blk = blockIdx.x % nsb;
+  const int64_t bk = blockIdx.x / nsb;
+  const int t0 = blk * sb, t1 = min(t0 + sb, L);
+  const int64_t e0 = bk * (int64_t)L * D + (int64_t)t0 * D;
+  const int nch = (t1 - t0) * D / 8;
+  const u32x4 *in = (const u32x4 *)(src + e0);
+  u32x4 v[NC];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int ch = threadIdx.x + 256 * i;
+    v[i] = ch < nch ? __builtin_nontemporal_load(in + ch) : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(v[i][j] << 16)),
+                               fabsf(__uint_as_float(v[i][j] & 0xffff0000u))));
+  }
+  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
+  if (threadIdx.x == 0) scales[bk * nsb + blk] = amax > 0.0f ? amax / 448.0f : 0.0f;
+  u32x2 *out = (u32x2 *)(codes + e0);
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int ch = threadIdx.x + 256 * i;
+    if (ch >= nch) break;
+    u32x2 c = {0, 0};
+    if (amax > 0.0f) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t p0 = v[i][2 * h], p1 = v[i][2 * h + 1];
+        int w = __builtin_amdgcn_cvt_pk_fp8_f32(__uint_as_float(p0 << 16) * inv,
+                                                __uint_as_float(p0 & 0xffff0000u) * inv, 0, false);
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(__uint_as_float(p1 << 16) * inv,
+                                            __uint_as_float(p1 & 0xffff0000u) * inv, w, true);
+        c[h] = (uint32_t)w;
+      }
+    }
+    out[ch] = c;
+  }
+}
+
+// general path (any head_dim or alignment, any block size): two passes
+// over the block with element loads and the software encoder
 __global__ __launch_bounds__(256) void kv_quantize(const uint16_t *src,
                                                    uint8_t *codes,
                                                    float *scales, int32_t L,
@@ -626,9 +687,21 @@ hipError_t launch_decode(const DecodeLaunch &L, hipStream_t s) {
 
 hipError_t launch_kv_quantize(const QuantLaunch &q, hipStream_t s) {
   const int grid = (int)(q.batch * q.heads_kv * q.n_scale_blocks);
-  hipLaunchKernelGGL(kv_quantize, dim3(grid), dim3(256), 0, s, (const uint16_t *)q.src,
-                     q.codes, q.scales, (int32_t)q.seq_kv, (int32_t)q.head_dim,
-                     (int32_t)q.scale_block, (int32_t)q.n_scale_blocks);
+  const uint16_t *src = (const uint16_t *)q.src;
+  const int32_t L = (int32_t)q.seq_kv, D = (int32_t)q.head_dim, sb = (int32_t)q.scale_block,
+                nsb = (int32_t)q.n_scale_blocks;
+  const int64_t chunks = q.scale_block * q.head_dim / 8;  // 8-element chunks per full block
+  const bool reg = q.head_dim % 8 == 0 && ((uintptr_t)q.src & 15u) == 0 &&
+                   ((uintptr_t)q.codes & 7u) == 0 && chunks <= 256 * QMAX;
+  if (reg && chunks <= 256 * 4)
+    hipLaunchKernelGGL(kv_quantize_reg<4>, dim3(grid), dim3(256), 0, s, src, q.codes, q.scales,
+                       L, D, sb, nsb);
+  else if (reg)
+    hipLaunchKernelGGL(kv_quantize_reg<QMAX>, dim3(grid), dim3(256), 0, s, src, q.codes,
+                       q.scales, L, D, sb, nsb);
+  else
+    hipLaunchKernelGGL(kv_quantize, dim3(grid), dim3(256), 0, s, src, q.codes, q.scales, L, D,
+                       sb, nsb);
   return hipGetLastError();
 }
 

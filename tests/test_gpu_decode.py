@@ -12,7 +12,7 @@ import pytest
 import torch
 
 import oracle
-from helpers import (TOL_BF16_ABS, TOL_FP8_ABS, TOL_LSE_ABS, bits, max_abs,
+from helpers import (TOL_BF16_ABS, TOL_FP8_ABS, TOL_LSE_ABS, bits, from_bf16_bits, max_abs,
                      randn, to_f32)
 
 pytestmark = pytest.mark.gpu
@@ -107,6 +107,45 @@ def test_kv_quantize_bit_exact(ops, L, sb):
     ref_codes, ref_scales = oracle.kv_quantize_fp8(bits(kv), sb)
     assert np.array_equal(codes.cpu().numpy(), ref_codes)
     assert np.array_equal(scales.cpu().numpy().view(np.uint32), ref_scales.view(np.uint32))
+
+
+def test_kv_quantize_every_bf16_value(ops):
+    """Every finite bf16 value of magnitude <= 448, both signs (ties, the
+    E4M3 subnormal range and signed zeros included), quantised with a block
+    scale of exactly 1 (each 64 x 128 block opens with 448): the codes must
+    equal the oracle's encoder bit for bit."""
+    _log("case: kv quantize exhaustive bf16")
+    pos = np.arange(0x0000, 0x43E1, dtype=np.uint16)
+    vals = np.concatenate([pos, pos | 0x8000])
+    per = 64 * 128 - 1
+    nblk = -(-vals.size // per)
+    flat = np.zeros(nblk * (per + 1), dtype=np.uint16)
+    for i in range(nblk):
+        chunk = vals[i * per:(i + 1) * per]
+        flat[i * (per + 1)] = 0x43E0
+        flat[i * (per + 1) + 1:i * (per + 1) + 1 + chunk.size] = chunk
+    src = flat.reshape(1, 1, nblk * 64, 128)
+    kv = from_bf16_bits(src)
+    codes, scales = ops.kv_quantize_fp8(kv.cuda(), scale_block=64)
+    torch.cuda.synchronize()
+    ref_codes, ref_scales = oracle.kv_quantize_fp8(src, 64)
+    assert (ref_scales == 1.0).all()
+    got = codes.cpu().numpy()
+    bad = np.flatnonzero(got != ref_codes)
+    assert bad.size == 0, [(hex(src.ravel()[i]), hex(got.ravel()[i]), hex(ref_codes.ravel()[i]))
+                           for i in bad[:8]]
+    assert np.array_equal(scales.cpu().numpy(), ref_scales)
+
+
+def test_kv_quantize_general_path(ops):
+    """head_dim 100 (not a multiple of 8) takes the element-wise kernel."""
+    _log("case: kv quantize head_dim 100")
+    kv = randn((1, 2, 300, 100), seed=13)
+    codes, scales = ops.kv_quantize_fp8(kv.cuda(), scale_block=64)
+    torch.cuda.synchronize()
+    ref_codes, ref_scales = oracle.kv_quantize_fp8(bits(kv), 64)
+    assert np.array_equal(codes.cpu().numpy(), ref_codes)
+    assert np.array_equal(scales.cpu().numpy(), ref_scales)
 
 
 @pytest.mark.parametrize("B,Hq,Hk,L,splits", [(2, 8, 2, 1000, 3), (2, 32, 8, 2048, 16)])
