@@ -25,8 +25,10 @@ __device__ inline const char *uniform_ptr(const char *p) {
   return (const char *)(uintptr_t)(((uint64_t)hi << 32) | lo);
 }
 
+// LDS byte address of a pointer into a __shared__ array: the low 32 bits of
+// its generic address (no null check), made wave-uniform
 __device__ inline uint32_t lds_offset(const uint8_t *p) {
-  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)as_lds(p));
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
 }
 
 // One global_load_lds_dwordx4: 16 bytes per lane into LDS at lds_addr +
@@ -36,58 +38,40 @@ __device__ inline uint32_t lds_offset(const uint8_t *p) {
 // serialising any prefetch. The compiler therefore does not count these
 // loads: callers wait for them explicitly (s_waitcnt vmcnt, plus a barrier
 // when other waves read the data) and finish their own reads of a slot
-// (lgkmcnt(0)) before refilling it. M0 is saved and restored around the
-// copy because the compiler treats it as reserved, not as a clobber.
+// (lgkmcnt(0)) before refilling it. The LDS address travels in M0 as a tied
+// input/output operand, so the compiler sets M0 itself (one s_mov) and knows
+// the statement leaves it changed; the s_nop covers the M0-write -> LDS-DMA
+// hazard, which the compiler does not check inside inline assembly.
 // NT = true marks the load non-temporal (streamed data read once: keeps it
 // from displacing reused lines, and measured on MI355X it sustains ~7.1 TB/s
 // against ~6.4 TB/s for plain loads).
 template <bool NT = false>
 __device__ inline void dma16(const char *sbase, uint32_t voff, uint32_t lds_addr) {
-  uint32_t saved;
+  uint32_t m0;
   if (NT)
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %3\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, %2 nt\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(voff), "s"(uniform_ptr(sbase)), "s"(lds_addr)
-        : "memory");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
+                 : "={m0}"(m0)
+                 : "v"(voff), "s"(uniform_ptr(sbase)), "0"(lds_addr)
+                 : "memory");
   else
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %3\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, %2\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(voff), "s"(uniform_ptr(sbase)), "s"(lds_addr)
-        : "memory");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 : "={m0}"(m0)
+                 : "v"(voff), "s"(uniform_ptr(sbase)), "0"(lds_addr)
+                 : "memory");
 }
 template <bool NT = false>
 __device__ inline void dma16(const char *addr, uint32_t lds_addr) {
-  uint32_t saved;
+  uint32_t m0;
   if (NT)
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %2\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, off nt\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(addr), "s"(lds_addr)
-        : "memory");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, off nt"
+                 : "={m0}"(m0)
+                 : "v"(addr), "0"(lds_addr)
+                 : "memory");
   else
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %2\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, off\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(addr), "s"(lds_addr)
-        : "memory");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 : "={m0}"(m0)
+                 : "v"(addr), "0"(lds_addr)
+                 : "memory");
 }
 
 // s_waitcnt immediates (gfx9 encoding): wait until at most n vector-memory
