@@ -51,12 +51,12 @@ __device__ inline void dma16(const char *sbase, uint32_t voff, uint32_t lds_addr
   if (NT)
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
                  : "={m0}"(m0)
-                 : "v"(voff), "s"(uniform_ptr(sbase)), "0"(lds_addr)
+                 : "v"(voff), "s"(uniform_ptr(sbase)), "0"(__builtin_amdgcn_readfirstlane(lds_addr))
                  : "memory");
   else
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                  : "={m0}"(m0)
-                 : "v"(voff), "s"(uniform_ptr(sbase)), "0"(lds_addr)
+                 : "v"(voff), "s"(uniform_ptr(sbase)), "0"(__builtin_amdgcn_readfirstlane(lds_addr))
                  : "memory");
 }
 template <bool NT = false>
@@ -65,12 +65,12 @@ __device__ inline void dma16(const char *addr, uint32_t lds_addr) {
   if (NT)
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, off nt"
                  : "={m0}"(m0)
-                 : "v"(addr), "0"(lds_addr)
+                 : "v"(addr), "0"(__builtin_amdgcn_readfirstlane(lds_addr))
                  : "memory");
   else
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
                  : "={m0}"(m0)
-                 : "v"(addr), "0"(lds_addr)
+                 : "v"(addr), "0"(__builtin_amdgcn_readfirstlane(lds_addr))
                  : "memory");
 }
 
