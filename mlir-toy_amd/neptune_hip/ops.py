@@ -64,12 +64,17 @@ def attention(
     return_lse: bool = False,
     out: torch.Tensor | None = None,
     lse: torch.Tensor | None = None,
+    scale_log2: float | None = None,
 ):
     """softmax(q k^T * scale) v with the HTile numeric policy.
 
     q [B, Hq, Sq, D], k/v [B, Hkv, Skv, D] in float32, float16 or bfloat16;
     returns out [B, Hq, Sq, D] (and lse [B, Hq, Sq] fp32 if asked).
+    ``scale_log2`` gives the score scale already in the exp2 domain (the
+    HTile program's own constant, HTile:24), in place of ``scale``.
     """
+    if scale is not None and scale_log2 is not None:
+        raise ValueError("give scale or scale_log2, not both")
     _require_cuda(q, k, v, out)
     if q.dtype not in _TORCH_TO_DTYPE or k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError(f"q, k, v must share one of {list(_TORCH_TO_DTYPE)}")
@@ -96,7 +101,7 @@ def attention(
     desc.o_stride[:] = _strides_bhs(out)
     desc.dtype = _TORCH_TO_DTYPE[q.dtype]
     desc.causal = 1 if causal else 0
-    desc.scale_log2 = scale_to_log2(scale, D)
+    desc.scale_log2 = float(scale_log2) if scale_log2 is not None else scale_to_log2(scale, D)
     lib = load_library()
     with torch.cuda.device(q.device):
         check(
