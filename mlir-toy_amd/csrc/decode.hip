@@ -30,6 +30,11 @@ namespace neptune {
 namespace {
 
 constexpr int STEP = 32;    // tokens per wave step
+// Lazy-rescale margin (log2 units): the running max only moves when a step's
+// max exceeds it by more than this; in between p = 2^(s - m) <= 2^kSlack,
+// which fp32 sums hold exactly as well and whose bf16 rounding is relative,
+// so results differ from a rescale at every step by rounding only.
+constexpr float kSlack = 8.0f;
 constexpr int DH = 128;     // head_dim covered by the decode kernels
 
 struct DecArgs {
@@ -42,10 +47,12 @@ struct DecArgs {
 };
 
 // bf16 bits of 4 E4M3 codes packed in one dword -> two dwords of bf16 pairs
+// (v_cvt_scalef32_pk_bf16_fp8 with scale 1: every E4M3 value is a bf16 value,
+// so the widening is exact)
 __device__ inline u32x2 e4m3x4_to_bf16(uint32_t c) {
-  f32x2 lo = e4m3x2_to_f32<false>(c);
-  f32x2 hi = e4m3x2_to_f32<true>(c);
-  return u32x2{Bf16Tag::pack2(lo[0], lo[1]), Bf16Tag::pack2(hi[0], hi[1])};
+  const bf16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c, 1.0f, false);
+  const bf16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c, 1.0f, true);
+  return u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
 }
 
 // bf16 KV through LDS: each wave streams its token range in 32-token steps
@@ -185,24 +192,26 @@ __global__ __launch_bounds__(RT) void decode_partial_ring(DecArgs a) {
       for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kb][r]);
     mx = wave_max_xor(mx, 16);
     mx = wave_max_xor(mx, 32);
-    const float m_new = fmaxf(m, mx);
-    const float alpha = fast_exp2(m - m_new);
-    float rs = 0.0f;
-    float p[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float e = fast_exp2(s[j >> 2][j & 3] - m_new);
-      rs += e;
-      p[j] = e;
-    }
-    lsum = lsum * alpha + rs;
-    m = m_new;
-    if (__any(alpha != 1.0f)) {
+    // lazy rescale: the running max moves only past a 2^kSlack margin
+    if (__any(mx > m + kSlack)) {
+      const float m_new = fmaxf(m, mx);
+      const float alpha = fast_exp2(m - m_new);
+      m = m_new;
+      lsum *= alpha;
 #pragma unroll
       for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) oacc[mb][r] *= alpha;
     }
+    float rs = 0.0f;
+    float p[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float e = fast_exp2(s[j >> 2][j & 3] - m);
+      rs += e;
+      p[j] = e;
+    }
+    lsum += rs;
     // P^T: k-slot 8 G + j holds key 4 G + j (j < 4) or 16 + 4 G + j - 4
     u32x4 pf;
 #pragma unroll
@@ -414,24 +423,26 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
       for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kb][r]);
     mx = wave_max_xor(mx, 16);
     mx = wave_max_xor(mx, 32);
-    const float m_new = fmaxf(m, mx);
-    const float alpha = fast_exp2(m - m_new);
-    float rs = 0.0f;
-    float p[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float e = fast_exp2(s[j >> 2][j & 3] - m_new);
-      rs += e;
-      p[j] = e;
-    }
-    lsum = lsum * alpha + rs;
-    m = m_new;
-    if (__any(alpha != 1.0f)) {
+    // lazy rescale: the running max moves only past a 2^kSlack margin
+    if (__any(mx > m + kSlack)) {
+      const float m_new = fmaxf(m, mx);
+      const float alpha = fast_exp2(m - m_new);
+      m = m_new;
+      lsum *= alpha;
 #pragma unroll
       for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) oacc[mb][r] *= alpha;
     }
+    float rs = 0.0f;
+    float p[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float e = fast_exp2(s[j >> 2][j & 3] - m);
+      rs += e;
+      p[j] = e;
+    }
+    lsum += rs;
     u32x4 pf;
 #pragma unroll
     for (int i2 = 0; i2 < 4; ++i2) pf[i2] = Bf16Tag::pack2(p[2 * i2] * vsc, p[2 * i2 + 1] * vsc);
