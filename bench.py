@@ -100,6 +100,33 @@ def bench_decode(ops, torch, steps, warmup, fp8):
     return name, wall, ev, nbytes
 
 
+def bench_decode_paged(ops, torch, steps, warmup, page_size=64):
+    """Config 3 with K/V held in a shuffled page pool, token-major pages
+    [pages, page_size, Hkv, D] (seen as [pages, Hkv, page_size, D]) and a
+    random block table: same bytes as contiguous decode, scattered in HBM."""
+    B, Hq, Hk, L, D, splits = 16, 32, 8, 32768, 128, 16
+    per = L // page_size
+    npages = B * per
+    g = torch.Generator(device="cuda").manual_seed(4)
+    q = torch.randn((B, Hq, D), device="cuda", generator=g).to(torch.bfloat16)
+    k_pool = torch.randn((npages, page_size, Hk, D), device="cuda", generator=g).to(torch.bfloat16)
+    v_pool = torch.randn((npages, page_size, Hk, D), device="cuda", generator=g).to(torch.bfloat16)
+    kp, vp = k_pool.permute(0, 2, 1, 3), v_pool.permute(0, 2, 1, 3)
+    table = torch.randperm(npages, device="cuda", generator=g).to(torch.int32).view(B, per)
+    lens = torch.full((B,), L, dtype=torch.int32, device="cuda")
+    k_meta = torch.empty((B, Hk, L, D), dtype=torch.bfloat16, device="meta")
+    ws = torch.empty(ops.decode_workspace_bytes(q, k_meta, num_splits=splits),
+                     dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+
+    def step(_):
+        ops.decode_paged(q, kp, vp, table, lens, max_seq_len=L, num_splits=splits, workspace=ws)
+
+    wall, ev = time_launches(step, steps, warmup)
+    nbytes = 2 * B * Hk * L * D * 2 + B * per * 4 + 2 * B * Hq * D * 2
+    return "config3 bf16 split-K GQA decode, paged KV (64-token pages)", wall, ev, nbytes
+
+
 def bench_scan(ops, torch, steps, warmup, rotate=2):
     Bn, L, Dm, N = 4, 2048, 5120, 16
     sets = []
@@ -202,7 +229,8 @@ def main():
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the decode/scan configurations")
     ap.add_argument("--workload", default="all",
-                    choices=["all", "prefill", "decode", "decode_fp8", "scan", "copy"],
+                    choices=["all", "prefill", "decode", "decode_fp8", "decode_paged", "scan",
+                             "copy"],
                     help="run one configuration only (for profiling); 'copy' is a plain "
                          "1 GiB device copy used to calibrate HBM byte counters")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
@@ -227,6 +255,7 @@ def main():
     single = {
         "decode": lambda: bench_decode(ops, torch, args.steps, args.warmup, fp8=False),
         "decode_fp8": lambda: bench_decode(ops, torch, args.steps, args.warmup, fp8=True),
+        "decode_paged": lambda: bench_decode_paged(ops, torch, args.steps, args.warmup),
         "scan": lambda: bench_scan(ops, torch, args.steps, args.warmup),
         "copy": lambda: bench_copy(torch, args.steps, args.warmup),
     }
@@ -250,6 +279,8 @@ def main():
         for key, fn in (("decode", lambda: bench_decode(ops, torch, sec_steps, sec_warm, False)),
                         ("decode_fp8", lambda: bench_decode(ops, torch, sec_steps, sec_warm,
                                                             True)),
+                        ("decode_paged", lambda: bench_decode_paged(ops, torch, sec_steps,
+                                                                    sec_warm)),
                         ("scan", lambda: bench_scan(ops, torch, sec_steps, sec_warm))):
             name, wall, ev, nbytes = fn()
             secondary.append(hbm_entry(key, name, wall, ev, nbytes, sec_steps, traffic))

@@ -108,6 +108,24 @@ typedef struct neptune_decode_desc {
   int32_t reserved;
 } neptune_decode_desc;
 
+/* Paged KV for split-K decode: K and V live in pools of fixed-size pages and
+ * sequence b's token t is in page block_table[b * max_pages + t / page_size]
+ * at position t % page_size. Element (page, kv head, position, d) of the K
+ * pool is at page * k_stride[0] + head * k_stride[1] + position * k_stride[2]
+ * + d (head_dim contiguous; the same for V), so both [pages, heads_kv,
+ * page_size, head_dim] and [pages, page_size, heads_kv, head_dim] pools are
+ * described. Sequence b has seq_lens[b] tokens (0 .. desc->seq_kv, the
+ * longest); an empty sequence yields O = 0 and lse = -inf. Block-table
+ * entries outside [0, num_pages) are clamped into range by the kernel (the
+ * results are then meaningless, but no memory outside the pools is read). */
+typedef struct neptune_paged_kv_desc {
+  int64_t num_pages;   /* pages in each pool                              */
+  int64_t page_size;   /* tokens per page, a multiple of 32               */
+  int64_t max_pages;   /* block-table row length, >= ceil(seq_kv/page)    */
+  int64_t k_stride[3]; /* elements: page, kv head, position               */
+  int64_t v_stride[3];
+} neptune_paged_kv_desc;
+
 /* Mamba-1 selective scan (Gu & Dao 2023, selective_scan_fn semantics):
  *   delta = softplus(delta_raw + delta_bias[d])   (if delta_softplus)
  *   x_n  <- exp(delta * A[d,n]) x_n + delta * B[b,n,l] * u[b,d,l]
@@ -158,6 +176,21 @@ NEPTUNE_API neptune_status neptune_kv_quantize_fp8(int64_t batch, int64_t heads_
                                        int64_t scale_block, const void *src,
                                        uint8_t *codes, float *scales,
                                        void *stream);
+
+/* Split-K decode over a paged KV cache (neptune_paged_kv_desc). No
+ * counterpart in the reference: the block-table layout of serving caches,
+ * consumed by the same split-K kernel. desc->kv_dtype must be BF16;
+ * desc->seq_kv is the longest sequence and sets the split layout (the
+ * workspace is sized by neptune_decode_workspace_bytes(desc)). block_table
+ * [batch, max_pages] and seq_lens [batch] are int32 device arrays. */
+NEPTUNE_API neptune_status neptune_decode_paged(const neptune_decode_desc *desc,
+                                    const neptune_paged_kv_desc *pages,
+                                    const void *q, const void *k_pages,
+                                    const void *v_pages,
+                                    const int32_t *block_table,
+                                    const int32_t *seq_lens, void *o, float *lse,
+                                    void *workspace, size_t workspace_bytes,
+                                    void *stream);
 
 /* ---- selective scan ---------------------------------------------------- */
 

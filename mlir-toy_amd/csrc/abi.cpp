@@ -203,17 +203,13 @@ neptune_status neptune_decode_workspace_bytes(const neptune_decode_desc *d, size
   return ok();
 }
 
-neptune_status neptune_decode_splitk(const neptune_decode_desc *d, const void *q,
-                                     const void *k, const void *v, const float *k_scale,
-                                     const float *v_scale, void *o, float *lse,
-                                     void *workspace, size_t workspace_bytes, void *stream) {
-  neptune_status st = decode_check(d);
-  if (st != NEPTUNE_OK) return st;
-  if (!q || !k || !v || !o)
-    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode: q, k, v and o must be non-NULL");
-  const bool fp8 = d->kv_dtype == NEPTUNE_DTYPE_FP8_E4M3;
-  if (fp8 && (!k_scale || !v_scale))
-    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode: fp8 KV needs k_scale and v_scale");
+namespace {
+// shared tail of the two decode entry points (pk != nullptr: paged KV)
+neptune_status decode_run(const neptune_decode_desc *d, const neptune_paged_kv_desc *pk,
+                          const void *q, const void *k, const void *v, const float *k_scale,
+                          const float *v_scale, const int32_t *block_table,
+                          const int32_t *seq_lens, void *o, float *lse, void *workspace,
+                          size_t workspace_bytes, void *stream) {
   if (!workspace) return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode: workspace is NULL");
   int64_t splits, chunk;
   decode_layout(d, &splits, &chunk);
@@ -235,14 +231,70 @@ neptune_status neptune_decode_splitk(const neptune_decode_desc *d, const void *q
   L.scale_log2 = d->scale_log2 != 0.0f
                      ? d->scale_log2
                      : (float)(1.4426950408889634 / std::sqrt((double)d->head_dim));
+  if (pk) {
+    L.block_table = block_table;
+    L.seq_lens = seq_lens;
+    L.page_size = pk->page_size;
+    L.max_pages = pk->max_pages;
+    L.num_pages = pk->num_pages;
+    for (int i = 0; i < 3; ++i) {
+      L.k_pstride[i] = pk->k_stride[i];
+      L.v_pstride[i] = pk->v_stride[i];
+    }
+  }
   const size_t rows = (size_t)d->batch * d->heads_q * splits;
   L.part_o = (float *)workspace;
   L.part_ml = (float *)((char *)workspace + align256(rows * d->head_dim * 4));
   const char *why = "";
   if (!decode_supported(L, &why)) return fail(NEPTUNE_ERR_UNSUPPORTED, "decode: %s", why);
-  st = device_ready();
+  neptune_status st = device_ready();
   if (st != NEPTUNE_OK) return st;
   return hip_result(launch_decode(L, (hipStream_t)stream), "decode launch");
+}
+}  // namespace
+
+neptune_status neptune_decode_splitk(const neptune_decode_desc *d, const void *q,
+                                     const void *k, const void *v, const float *k_scale,
+                                     const float *v_scale, void *o, float *lse,
+                                     void *workspace, size_t workspace_bytes, void *stream) {
+  neptune_status st = decode_check(d);
+  if (st != NEPTUNE_OK) return st;
+  if (!q || !k || !v || !o)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode: q, k, v and o must be non-NULL");
+  const bool fp8 = d->kv_dtype == NEPTUNE_DTYPE_FP8_E4M3;
+  if (fp8 && (!k_scale || !v_scale))
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode: fp8 KV needs k_scale and v_scale");
+  return decode_run(d, nullptr, q, k, v, k_scale, v_scale, nullptr, nullptr, o, lse, workspace,
+                    workspace_bytes, stream);
+}
+
+neptune_status neptune_decode_paged(const neptune_decode_desc *d, const neptune_paged_kv_desc *pk,
+                                    const void *q, const void *k_pages, const void *v_pages,
+                                    const int32_t *block_table, const int32_t *seq_lens, void *o,
+                                    float *lse, void *workspace, size_t workspace_bytes,
+                                    void *stream) {
+  neptune_status st = decode_check(d);
+  if (st != NEPTUNE_OK) return st;
+  if (!pk) return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode_paged: pages desc is NULL");
+  if (!q || !k_pages || !v_pages || !block_table || !seq_lens || !o)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT,
+                "decode_paged: q, pools, block_table, seq_lens and o must be non-NULL");
+  if (d->kv_dtype != NEPTUNE_DTYPE_BF16)
+    return fail(NEPTUNE_ERR_UNSUPPORTED, "decode_paged: kv_dtype must be BF16");
+  if (pk->num_pages <= 0 || pk->page_size <= 0 || pk->max_pages <= 0)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT,
+                "decode_paged: num_pages, page_size and max_pages must be positive");
+  if (pk->max_pages * pk->page_size < d->seq_kv)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT,
+                "decode_paged: max_pages (%lld) * page_size (%lld) < seq_kv (%lld)",
+                (long long)pk->max_pages, (long long)pk->page_size, (long long)d->seq_kv);
+  for (int i = 0; i < 3; ++i)
+    if (pk->k_stride[i] <= 0 || pk->v_stride[i] <= 0 || pk->k_stride[i] % 8 ||
+        pk->v_stride[i] % 8)
+      return fail(NEPTUNE_ERR_UNSUPPORTED,
+                  "decode_paged: pool strides must be positive multiples of 8 elements");
+  return decode_run(d, pk, q, k_pages, v_pages, nullptr, nullptr, block_table, seq_lens, o, lse,
+                    workspace, workspace_bytes, stream);
 }
 
 neptune_status neptune_kv_quantize_fp8(int64_t batch, int64_t heads_kv, int64_t seq_kv,

@@ -44,6 +44,12 @@ struct DecArgs {
   float *part_o, *part_ml;
   int32_t Hq, Hk, group, L, chunk, splits, nsb, sb;
   float scale2;
+  // paged KV (decode_partial_ring<true>): token t of sequence b lives in page
+  // btab[b * maxp + t / ps], at element offset page * k_ps[0] + head * k_ps[1]
+  // + (t % ps) * tok (the same for V with v_ps); seqlens[b] tokens
+  const int32_t *btab, *seqlens;
+  int32_t ps, maxp, npages, tok;
+  int64_t k_ps[2], v_ps[2];
 };
 
 // bf16 bits of 4 E4M3 codes packed in one dword -> two dwords of bf16 pairs
@@ -73,6 +79,7 @@ constexpr int RW = 1;                       // waves per work-group (LDS-bound o
 constexpr int RT = 64 * RW;                 // threads per work-group
 constexpr int RLDS = RW * RWAVE;
 
+template <bool PAGED>
 __global__ __launch_bounds__(RT) void decode_partial_ring(DecArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -83,47 +90,71 @@ __global__ __launch_bounds__(RT) void decode_partial_ring(DecArgs a) {
   const int bk = id / a.splits;  // batch * Hk + kv head
   const int b = bk / a.Hk, hk = bk % a.Hk;
   const int Gq = a.group;
+  // this sequence's length (paged: its own; out-of-range values clamped)
+  const int Lb = PAGED ? min(max(a.seqlens[b], 0), a.L) : a.L;
 
   const int c0 = split * a.chunk;
-  const int c1 = min(c0 + a.chunk, a.L);
+  const int c1 = min(c0 + a.chunk, Lb);
   const int wlen = ((a.chunk + RW * RSTEP - 1) / (RW * RSTEP)) * RSTEP;
   const int t0 = c0 + w * wlen;
   const int t1 = min(t0 + wlen, c1);
   const int nsteps = t1 > t0 ? (t1 - t0 + RSTEP - 1) / RSTEP : 0;
 
   const uint8_t *ring = smem + w * RWAVE;
-  const char *kbase = (const char *)a.k + (int64_t)bk * a.L * DH * 2;
-  const char *vbase = (const char *)a.v + (int64_t)bk * a.L * DH * 2;
+  // token-row stride in bytes; contiguous KV: row t of (b, kv head) at
+  // (bk * L + t) * DH elements
+  const int64_t tokb = PAGED ? (int64_t)a.tok * 2 : DH * 2;
+  const char *kbase = (const char *)a.k + (PAGED ? (int64_t)hk * a.k_ps[1] * 2
+                                                 : (int64_t)bk * a.L * DH * 2);
+  const char *vbase = (const char *)a.v + (PAGED ? (int64_t)hk * a.v_ps[1] * 2
+                                                 : (int64_t)bk * a.L * DH * 2);
+  // bytes from kbase / vbase to the first row of the 32-token step at tb: a
+  // step never straddles a page (the page size is a multiple of 32 and steps
+  // start on multiples of 32); a block-table entry outside [0, npages) is
+  // clamped so that a bad table cannot address memory outside the pages
+  auto step_base = [&](int tb, int64_t *kb, int64_t *vb) {
+    if (PAGED) {
+      int pg = a.btab[(int64_t)b * a.maxp + tb / a.ps];
+      pg = min(max(pg, 0), a.npages - 1);
+      const int64_t in_page = (int64_t)(tb % a.ps) * tokb;
+      *kb = (int64_t)pg * a.k_ps[0] * 2 + in_page;
+      *vb = (int64_t)pg * a.v_ps[0] * 2 + in_page;
+    } else {
+      *kb = *vb = (int64_t)tb * DH * 2;
+    }
+  };
   // per-lane byte offsets of this lane's 16 bytes in DMA chunk c (rows 4c + G)
   uint32_t koff[8], voff[8];
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
     const int r = 4 * c + G;
-    koff[c] = (uint32_t)(r * DH * 2 + (((lane & 15) ^ (r & 15)) << 4));
-    voff[c] = (uint32_t)(r * DH * 2 + (((lane & 15) ^ (2 * (r & 7))) << 4));
+    koff[c] = (uint32_t)(r * tokb + (((lane & 15) ^ (r & 15)) << 4));
+    voff[c] = (uint32_t)(r * tokb + (((lane & 15) ^ (2 * (r & 7))) << 4));
   }
   auto issue = [&](int i) {
     const int tb = t0 + i * RSTEP;
     const uint8_t *slot = ring + (i & 1) * RSLOT;
-    if (tb + RSTEP <= a.L) {
-      const char *kb = kbase + (int64_t)tb * DH * 2, *vb = vbase + (int64_t)tb * DH * 2;
+    int64_t kb0, vb0;
+    step_base(tb, &kb0, &vb0);
+    if (tb + RSTEP <= Lb) {
+      const char *kb = kbase + kb0, *vb = vbase + vb0;
 #pragma unroll
       for (int c = 0; c < 8; ++c) dma16<true>(kb, koff[c], lds_offset(slot + c * 1024));
 #pragma unroll
       for (int c = 0; c < 8; ++c) dma16<true>(vb, voff[c], lds_offset(slot + RTILE + c * 1024));
-    } else {  // tail: rows past the sequence re-read the last token (masked)
+    } else {  // tail: rows past the sequence re-read its last token (masked)
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
         const int r = 4 * c + G;
-        const int64_t row = min(tb + r, a.L - 1);
-        dma16<true>(kbase + row * DH * 2 + (((lane & 15) ^ (r & 15)) << 4),
+        const int64_t row = min(tb + r, Lb - 1) - tb;
+        dma16<true>(kbase + kb0 + row * tokb + (((lane & 15) ^ (r & 15)) << 4),
               lds_offset(slot + c * 1024));
       }
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
         const int r = 4 * c + G;
-        const int64_t row = min(tb + r, a.L - 1);
-        dma16<true>(vbase + row * DH * 2 + (((lane & 15) ^ (2 * (r & 7))) << 4),
+        const int64_t row = min(tb + r, Lb - 1) - tb;
+        dma16<true>(vbase + vb0 + row * tokb + (((lane & 15) ^ (2 * (r & 7))) << 4),
               lds_offset(slot + RTILE + c * 1024));
       }
     }
@@ -535,8 +566,9 @@ __global__ __launch_bounds__(DH) void decode_combine(const float *part_o,
 #pragma unroll 8
   for (int s = 0; s < splits; ++s) acc += wts[s] * po[(int64_t)s * DH];
   const float Ls = stat[1];
-  o[bh * DH + d] = Bf16Tag::from_f32(acc / Ls);
-  if (d == 0 && lse) lse[bh] = (stat[0] + log2f(Ls)) * kLn2;
+  // an empty sequence (paged decode with length 0) has L = 0: O = 0, lse = -inf
+  o[bh * DH + d] = Bf16Tag::from_f32(Ls > 0.0f ? acc / Ls : 0.0f);
+  if (d == 0 && lse) lse[bh] = Ls > 0.0f ? (stat[0] + log2f(Ls)) * kLn2 : -INFINITY;
 }
 
 // One work-group per (batch, kv head, scale block): amax, scale, codes.
@@ -641,6 +673,21 @@ bool decode_supported(const DecodeLaunch &a, const char **why) {
     *why = "fp8 decode needs scale_block to be a multiple of 32 tokens";
     return false;
   }
+  if (a.block_table) {
+    if (a.kv_dtype == 3) {
+      *why = "paged decode supports bf16 KV";
+      return false;
+    }
+    if (a.page_size % STEP) {
+      *why = "paged decode needs a page size that is a multiple of 32 tokens";
+      return false;
+    }
+    if (a.k_pstride[2] != a.v_pstride[2] || 31 * a.k_pstride[2] * 2 + 256 > ((int64_t)1 << 31) ||
+        a.num_pages > ((int64_t)1 << 31) - 1 || a.max_pages > ((int64_t)1 << 31) - 1) {
+      *why = "paged decode needs equal K/V token strides below 64 MiB and fewer than 2^31 pages";
+      return false;
+    }
+  }
   if (a.seq_kv > (int64_t)1 << 30 ||
       a.batch * a.heads_kv * a.splits > (int64_t)1 << 30) {
     *why = "decode shape too large for one launch";
@@ -667,6 +714,17 @@ hipError_t launch_decode(const DecodeLaunch &L, hipStream_t s) {
   a.nsb = (int32_t)L.n_scale_blocks;
   a.sb = (int32_t)L.scale_block;
   a.scale2 = L.scale_log2;
+  const bool paged = L.block_table != nullptr;
+  a.btab = L.block_table;
+  a.seqlens = L.seq_lens;
+  a.ps = (int32_t)L.page_size;
+  a.maxp = (int32_t)L.max_pages;
+  a.npages = (int32_t)L.num_pages;
+  a.tok = (int32_t)L.k_pstride[2];
+  a.k_ps[0] = L.k_pstride[0];
+  a.k_ps[1] = L.k_pstride[1];
+  a.v_ps[0] = L.v_pstride[0];
+  a.v_ps[1] = L.v_pstride[1];
   const int grid = (int)(L.batch * L.heads_kv * L.splits);
   if (L.kv_dtype == 3) {
     static bool attr8_set = false;  // benign race: the attribute is idempotent
@@ -678,14 +736,18 @@ hipError_t launch_decode(const DecodeLaunch &L, hipStream_t s) {
     }
     hipLaunchKernelGGL(decode_partial_ring8, dim3(grid), dim3(R8T), R8LDS, s, a);
   } else {
-    static bool attr_set = false;  // benign race: the attribute is idempotent
-    if (!attr_set) {
-      hipError_t e = hipFuncSetAttribute((const void *)decode_partial_ring,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, RLDS);
+    static bool attr_set[2] = {false, false};  // benign race: the attribute is idempotent
+    const void *fn = paged ? (const void *)decode_partial_ring<true>
+                           : (const void *)decode_partial_ring<false>;
+    if (!attr_set[paged]) {
+      hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, RLDS);
       if (e != hipSuccess) return e;
-      attr_set = true;
+      attr_set[paged] = true;
     }
-    hipLaunchKernelGGL(decode_partial_ring, dim3(grid), dim3(RT), RLDS, s, a);
+    if (paged)
+      hipLaunchKernelGGL(decode_partial_ring<true>, dim3(grid), dim3(RT), RLDS, s, a);
+    else
+      hipLaunchKernelGGL(decode_partial_ring<false>, dim3(grid), dim3(RT), RLDS, s, a);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

@@ -29,6 +29,11 @@ struct DecodeLaunch {
   int64_t splits, chunk, scale_block, n_scale_blocks;
   int32_t kv_dtype;
   float scale_log2;
+  // paged KV (block_table != nullptr): k/v are page pools; seq_kv is the
+  // longest sequence, seq_lens[b] each sequence's length
+  const int32_t *block_table = nullptr, *seq_lens = nullptr;
+  int64_t page_size = 0, max_pages = 0, num_pages = 0;
+  int64_t k_pstride[3] = {0, 0, 0}, v_pstride[3] = {0, 0, 0};  // page, head, token (elements)
 };
 
 struct QuantLaunch {

@@ -40,8 +40,12 @@ __device__ inline uint32_t lds_offset(const uint8_t *p) {
 // when other waves read the data) and finish their own reads of a slot
 // (lgkmcnt(0)) before refilling it. The LDS address travels in M0 as a tied
 // input/output operand, so the compiler sets M0 itself (one s_mov) and knows
-// the statement leaves it changed; the s_nop covers the M0-write -> LDS-DMA
-// hazard, which the compiler does not check inside inline assembly.
+// the statement leaves it changed. The compiler does not check hazards
+// inside inline assembly, so the statement covers two itself: M0 write ->
+// LDS DMA (1 wait state) and, in the SGPR-base form, VALU write of an SGPR
+// (v_readfirstlane of the base) -> VMEM read of that SGPR (5 wait states:
+// s_nop 4). Without the latter a base computed by a VALU just before the
+// copy (a block-table lookup) is read stale.
 // NT = true marks the load non-temporal (streamed data read once: keeps it
 // from displacing reused lines, and measured on MI355X it sustains ~7.1 TB/s
 // against ~6.4 TB/s for plain loads).
@@ -49,12 +53,12 @@ template <bool NT = false>
 __device__ inline void dma16(const char *sbase, uint32_t voff, uint32_t lds_addr) {
   uint32_t m0;
   if (NT)
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
+    asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %1, %2 nt"
                  : "={m0}"(m0)
                  : "v"(voff), "s"(uniform_ptr(sbase)), "0"(__builtin_amdgcn_readfirstlane(lds_addr))
                  : "memory");
   else
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+    asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %1, %2"
                  : "={m0}"(m0)
                  : "v"(voff), "s"(uniform_ptr(sbase)), "0"(__builtin_amdgcn_readfirstlane(lds_addr))
                  : "memory");

@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "neptune_attn_fwd",
     "neptune_decode_workspace_bytes",
     "neptune_decode_splitk",
+    "neptune_decode_paged",
     "neptune_kv_quantize_fp8",
     "neptune_selective_scan_fwd",
 )
@@ -88,6 +89,18 @@ class DecodeDesc(ctypes.Structure):
         ("kv_dtype", ctypes.c_int32),
         ("scale_log2", ctypes.c_float),
         ("reserved", ctypes.c_int32),
+    ]
+
+
+class PagedKvDesc(ctypes.Structure):
+    """include/neptune_hip.h: neptune_paged_kv_desc"""
+
+    _fields_ = [
+        ("num_pages", ctypes.c_int64),
+        ("page_size", ctypes.c_int64),
+        ("max_pages", ctypes.c_int64),
+        ("k_stride", ctypes.c_int64 * 3),
+        ("v_stride", ctypes.c_int64 * 3),
     ]
 
 
@@ -198,6 +211,11 @@ def _declare(lib: ctypes.CDLL) -> None:
         ctypes.POINTER(DecodeDesc), vp, vp, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp,
     ]
     lib.neptune_decode_splitk.restype = i32
+    lib.neptune_decode_paged.argtypes = [
+        ctypes.POINTER(DecodeDesc), ctypes.POINTER(PagedKvDesc), vp, vp, vp, vp, vp, vp, vp, vp,
+        ctypes.c_size_t, vp,
+    ]
+    lib.neptune_decode_paged.restype = i32
     lib.neptune_kv_quantize_fp8.argtypes = [i64, i64, i64, i64, i64, vp, vp, vp, vp]
     lib.neptune_kv_quantize_fp8.restype = i32
     lib.neptune_selective_scan_fwd.argtypes = [

@@ -210,6 +210,71 @@ def decode_splitk(
     return (out, lse) if return_lse else out
 
 
+def decode_paged(
+    q: torch.Tensor,
+    k_pages: torch.Tensor,
+    v_pages: torch.Tensor,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    *,
+    max_seq_len: int | None = None,
+    num_splits: int = 0,
+    scale: float | None = None,
+    return_lse: bool = False,
+    workspace: torch.Tensor | None = None,
+):
+    """Split-K decode over a paged KV cache.
+
+    q [B, Hq, D] bf16; k_pages / v_pages bf16 [num_pages, Hkv, page_size, D]
+    views (any page/head/position strides with D contiguous, e.g. a permuted
+    [num_pages, page_size, Hkv, D] pool); block_table [B, max_pages] and
+    seq_lens [B] int32 on the device. ``max_seq_len`` (default
+    max_pages * page_size) is the longest sequence and sets the split
+    layout. Returns o [B, Hq, D] bf16.
+    """
+    q3 = _as_q3(q)
+    _require_cuda(q3, k_pages, v_pages, block_table, seq_lens, workspace)
+    if q3.dtype != torch.bfloat16 or k_pages.dtype != torch.bfloat16 or \
+            v_pages.dtype != torch.bfloat16:
+        raise ValueError("paged decode takes bfloat16 q and KV pages")
+    if k_pages.dim() != 4 or tuple(k_pages.shape) != tuple(v_pages.shape) or \
+            k_pages.stride(-1) != 1 or v_pages.stride(-1) != 1:
+        raise ValueError("k_pages / v_pages: matching [pages, Hkv, page_size, D] views, D contiguous")
+    for name, t in (("block_table", block_table), ("seq_lens", seq_lens)):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous int32 tensor")
+    npages, Hk, psize, D = k_pages.shape
+    B = q3.shape[0]
+    if block_table.dim() != 2 or block_table.shape[0] != B or tuple(seq_lens.shape) != (B,):
+        raise ValueError("block_table [B, max_pages] and seq_lens [B] must match q's batch")
+    max_pages = block_table.shape[1]
+    L = int(max_seq_len) if max_seq_len is not None else max_pages * psize
+    k4 = torch.empty((B, Hk, L, D), dtype=k_pages.dtype, device="meta")
+    desc = _decode_desc(q3, k4, num_splits, 64, scale, _abi.DTYPE_BF16)
+    pk = _abi.PagedKvDesc()
+    pk.num_pages, pk.page_size, pk.max_pages = npages, psize, max_pages
+    pk.k_stride[:] = (k_pages.stride(0), k_pages.stride(1), k_pages.stride(2))
+    pk.v_stride[:] = (v_pages.stride(0), v_pages.stride(1), v_pages.stride(2))
+    lib = load_library()
+    n = ctypes.c_size_t()
+    check(lib.neptune_decode_workspace_bytes(ctypes.byref(desc), ctypes.byref(n)), lib)
+    if workspace is None:
+        workspace = torch.empty(max(n.value, 1), dtype=torch.uint8, device=q3.device)
+    out = torch.empty_like(q3)
+    lse = torch.empty(q3.shape[:2], dtype=torch.float32, device=q3.device) if return_lse else None
+    with torch.cuda.device(q3.device):
+        check(
+            lib.neptune_decode_paged(
+                ctypes.byref(desc), ctypes.byref(pk), q3.data_ptr(), k_pages.data_ptr(),
+                v_pages.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(), out.data_ptr(),
+                lse.data_ptr() if lse is not None else None, workspace.data_ptr(),
+                workspace.numel() * workspace.element_size(), _stream(q3),
+            ),
+            lib,
+        )
+    return (out, lse) if return_lse else out
+
+
 def kv_quantize_fp8(kv: torch.Tensor, *, scale_block: int = 64):
     """bf16 [B, Hkv, L, D] -> (E4M3 codes uint8, scales fp32 [B, Hkv, nblocks])."""
     _require_cuda(kv)

@@ -87,6 +87,9 @@ int main(void) {
   F(neptune_decode_desc, num_splits) F(neptune_decode_desc, scale_block)
   F(neptune_decode_desc, q_dtype) F(neptune_decode_desc, kv_dtype)
   F(neptune_decode_desc, scale_log2) F(neptune_decode_desc, reserved) S(neptune_decode_desc)
+  F(neptune_paged_kv_desc, num_pages) F(neptune_paged_kv_desc, page_size)
+  F(neptune_paged_kv_desc, max_pages) F(neptune_paged_kv_desc, k_stride)
+  F(neptune_paged_kv_desc, v_stride) S(neptune_paged_kv_desc)
   F(neptune_scan_desc, batch) F(neptune_scan_desc, dim) F(neptune_scan_desc, seq_len)
   F(neptune_scan_desc, d_state) F(neptune_scan_desc, io_dtype)
   F(neptune_scan_desc, delta_softplus) S(neptune_scan_desc)
@@ -114,6 +117,7 @@ def test_ctypes_descriptors_match_the_c_header(tmp_path):
     pairs = [("neptune_attn_desc", _abi.AttnDesc, oracle.AttnDesc),
              ("neptune_decode_desc", _abi.DecodeDesc, oracle.DecodeDesc),
              ("neptune_scan_desc", _abi.ScanDesc, oracle.ScanDesc),
+             ("neptune_paged_kv_desc", _abi.PagedKvDesc, None),
              ("neptune_backend_info", _abi.BackendInfo, None)]
     for cname, prod, orc in pairs:
         for cls in (prod, orc):
@@ -228,6 +232,53 @@ def test_decode_workspace_and_fp8_errors(lib):
     assert _decode(lib, _dec_desc(kv_dtype=_abi.DTYPE_FP8_E4M3, scale_block=48),
                    kscale=FAKE) == _abi.ERR_UNSUPPORTED              # not a multiple of 32
     assert _decode(lib, _dec_desc(), ptrs=(FAKE, FAKE, 0)) == _abi.ERR_INVALID_ARGUMENT
+
+
+def _pages(**kw):
+    p = _abi.PagedKvDesc()
+    p.num_pages, p.page_size, p.max_pages = 64, 64, 32
+    p.k_stride[:] = (2 * 64 * 128, 64 * 128, 128)
+    p.v_stride[:] = (2 * 64 * 128, 64 * 128, 128)
+    for k, v in kw.items():
+        if k in ("k_stride", "v_stride"):
+            getattr(p, k)[:] = v
+        else:
+            setattr(p, k, v)
+    return p
+
+
+def _paged(lib, d, p, ws_bytes=1 << 30, ptrs=(FAKE,) * 5):
+    return lib.neptune_decode_paged(ctypes.byref(d), ctypes.byref(p) if p is not None else None,
+                                    *ptrs, FAKE, None, FAKE, ws_bytes, None)
+
+
+@pytest.mark.parametrize("dkw,pkw,status", [
+    ({}, {"page_size": 48}, _abi.ERR_UNSUPPORTED),                 # not a multiple of 32
+    ({}, {"max_pages": 15}, _abi.ERR_INVALID_ARGUMENT),             # 15 * 64 < seq_kv 1000
+    ({}, {"num_pages": 0}, _abi.ERR_INVALID_ARGUMENT),
+    ({}, {"k_stride": (100, 64 * 128, 128)}, _abi.ERR_UNSUPPORTED),  # not a multiple of 8
+    ({}, {"v_stride": (2 * 64 * 128, 64 * 128, 256)}, _abi.ERR_UNSUPPORTED),  # K/V token strides
+    ({"kv_dtype": _abi.DTYPE_FP8_E4M3}, {}, _abi.ERR_UNSUPPORTED),
+    ({"heads_q": 5}, {}, _abi.ERR_INVALID_ARGUMENT),
+])
+def test_paged_decode_validation(lib, dkw, pkw, status):
+    assert _paged(lib, _dec_desc(**dkw), _pages(**pkw)) == status
+    assert lib.neptune_last_error()
+
+
+def test_paged_decode_null_arguments(lib):
+    assert _paged(lib, _dec_desc(), None) == _abi.ERR_INVALID_ARGUMENT
+    for i in range(5):
+        ptrs = [FAKE] * 5
+        ptrs[i] = None
+        assert _paged(lib, _dec_desc(), _pages(), ptrs=tuple(ptrs)) == _abi.ERR_INVALID_ARGUMENT
+    assert _paged(lib, _dec_desc(), _pages(), ws_bytes=16) == _abi.ERR_WORKSPACE_TOO_SMALL
+
+
+def test_paged_decode_no_device_path(lib):
+    if lib.neptune_device_count() > 0:
+        pytest.skip("a HIP device is visible; the no-device path is not reachable")
+    assert _paged(lib, _dec_desc(), _pages()) == _abi.ERR_NO_DEVICE
 
 
 def test_quantize_and_scan_validation(lib):

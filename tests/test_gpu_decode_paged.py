@@ -1,0 +1,114 @@
+"""GPU parity of split-K decode over a paged KV cache (neptune_decode_paged).
+
+* With every sequence at the full length, paged decode over a shuffled page
+  pool equals contiguous decode of the same tokens bit for bit (same kernel
+  arithmetic, only the addressing differs), for both pool layouts
+  ([pages, Hkv, page, D] and [pages, page, Hkv, D] seen through a view).
+* Ragged lengths: each sequence against the oracle on its own tokens.
+* A zero-length sequence gives O = 0 and lse = -inf; block-table entries
+  outside the pool are clamped by the kernel (finite output, no fault).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import TOL_BF16_ABS, TOL_LSE_ABS, bits, randn, to_f32
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ops():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    from neptune_hip import ops as _ops
+    return _ops
+
+
+def _log(msg):
+    print(msg, flush=True)
+
+
+def paginate(kv, ps, seed, token_major=False, spare=3):
+    """Scatter contiguous [B, Hk, L, D] into a shuffled page pool. Returns the
+    pool view [pages, Hk, ps, D] and the block table [B, L / ps]."""
+    B, Hk, L, D = kv.shape
+    per = -(-L // ps)
+    npages = B * per + spare
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randperm(npages, generator=g)[: B * per].view(B, per).to(torch.int32)
+    if token_major:
+        pool = torch.zeros((npages, ps, Hk, D), dtype=kv.dtype)
+    else:
+        pool = torch.zeros((npages, Hk, ps, D), dtype=kv.dtype)
+    for b in range(B):
+        for j in range(per):
+            blk = kv[b, :, j * ps:(j + 1) * ps]
+            n = blk.shape[1]
+            if token_major:
+                pool[ids[b, j], :n] = blk.transpose(0, 1)
+            else:
+                pool[ids[b, j], :, :n] = blk
+    pool = pool.cuda()
+    view = pool.permute(0, 2, 1, 3) if token_major else pool
+    return view, ids.cuda()
+
+
+@pytest.mark.parametrize("token_major", [False, True])
+def test_paged_equals_contiguous_bitwise(ops, token_major):
+    _log(f"case: paged == contiguous, token_major={token_major}")
+    B, Hq, Hk, L, D, ps, splits = 2, 8, 2, 1024, 128, 64, 5
+    q = randn((B, Hq, D), seed=20).cuda()
+    k, v = randn((B, Hk, L, D), seed=21), randn((B, Hk, L, D), seed=22)
+    kp, table = paginate(k, ps, seed=23, token_major=token_major)
+    vp, _ = paginate(v, ps, seed=23, token_major=token_major)
+    lens = torch.full((B,), L, dtype=torch.int32, device="cuda")
+    o_ref, lse_ref = ops.decode_splitk(q, k.cuda(), v.cuda(), num_splits=splits, return_lse=True)
+    o, lse = ops.decode_paged(q, kp, vp, table, lens, max_seq_len=L, num_splits=splits,
+                              return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o.view(torch.int16), o_ref.view(torch.int16))
+    assert torch.equal(lse, lse_ref)
+
+
+def test_paged_ragged_lengths_match_oracle(ops):
+    _log("case: paged ragged lengths")
+    B, Hq, Hk, L, D, ps = 3, 8, 2, 1000, 128, 128
+    lens = [1000, 37, 513]
+    q = randn((B, Hq, D), seed=30)
+    k, v = randn((B, Hk, L, D), seed=31), randn((B, Hk, L, D), seed=32)
+    kp, table = paginate(k, ps, seed=33)
+    vp, _ = paginate(v, ps, seed=33)
+    o, lse = ops.decode_paged(q.cuda(), kp, vp, table,
+                              torch.tensor(lens, dtype=torch.int32, device="cuda"),
+                              max_seq_len=L, num_splits=4, return_lse=True)
+    torch.cuda.synchronize()
+    for b, n in enumerate(lens):
+        ro, rl, _ = oracle.decode_splitk(bits(q[b:b + 1]), bits(k[b:b + 1, :, :n]),
+                                         bits(v[b:b + 1, :, :n]), oracle.BF16, num_splits=1)
+        ref = oracle.decode(ro, oracle.BF16)[0]
+        got = to_f32(o[b])
+        err = np.abs(got - ref).max()
+        assert err <= TOL_BF16_ABS and err <= 2e-2 * np.abs(ref).max(), (b, err)
+        assert np.abs(to_f32(lse[b]) - rl[0]).max() <= TOL_LSE_ABS
+
+
+def test_paged_empty_sequence_and_bad_table(ops):
+    _log("case: paged empty sequence, out-of-range table entries")
+    B, Hq, Hk, L, D, ps = 2, 4, 1, 256, 128, 64
+    q = randn((B, Hq, D), seed=40).cuda()
+    k, v = randn((B, Hk, L, D), seed=41), randn((B, Hk, L, D), seed=42)
+    kp, table = paginate(k, ps, seed=43)
+    vp, _ = paginate(v, ps, seed=43)
+    lens = torch.tensor([0, L], dtype=torch.int32, device="cuda")
+    o, lse = ops.decode_paged(q, kp, vp, table, lens, max_seq_len=L, return_lse=True)
+    torch.cuda.synchronize()
+    assert (to_f32(o[0]) == 0).all() and torch.isinf(lse[0]).all() and (lse[0] < 0).all()
+    assert torch.isfinite(o[1].float()).all()
+    bad = table.clone()
+    bad[1, 0], bad[1, 1] = -5, 10 ** 6
+    o2 = ops.decode_paged(q, kp, vp, bad, lens, max_seq_len=L)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o2.float()).all()

@@ -1,0 +1,135 @@
+"""gfx950 hazards that the compiler does not check inside inline assembly.
+
+The HBM -> LDS copies (``global_load_lds_dwordx4``) are inline assembly
+(``mlir-toy_amd/csrc/lds_dma.h``), so LLVM's hazard recognizer does not see
+them, and the assembly itself must cover two hazards:
+
+* a VALU write of an SGPR (``v_readfirstlane_b32`` of the copy's base) read
+  by a VMEM instruction needs 5 wait states;
+* an SALU write of M0 read by an LDS DMA needs 1 wait state.
+
+Each wait state is one issued instruction (``s_nop N`` gives N + 1). This
+test compiles every kernel source to gfx950 assembly with the build's own
+flags. For every copy it then walks back over the instructions that precede
+it in program order. It pins a paged-decode bug in which a base looked up
+in the block table was written by ``v_readfirstlane`` two instructions
+before the copy that read it. The copy saw the previous base and loaded
+another step's tokens, with no fault.
+"""
+
+from __future__ import annotations
+
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+CSRC = Path(__file__).resolve().parents[1] / "mlir-toy_amd" / "csrc"
+HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+SOURCES = sorted(CSRC.glob("*.hip"))
+
+VALU_SGPR_TO_VMEM = 5
+M0_TO_LDS_DMA = 1
+
+
+def _build_flags() -> list[str]:
+    """HIPFLAGS of the library's Makefile (continuation lines joined)."""
+    text = (CSRC / "Makefile").read_text().replace("\\\n", " ")
+    m = re.search(r"^HIPFLAGS\s*\?=\s*(.+)$", text, re.M)
+    assert m, "HIPFLAGS not found in the Makefile"
+    return m.group(1).split()
+
+
+def _sgprs(tok: str) -> set[int]:
+    m = re.fullmatch(r"s\[(\d+):(\d+)\]", tok)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.fullmatch(r"s(\d+)", tok)
+    return {int(m.group(1))} if m else set()
+
+
+def _instructions(asm: str) -> list[tuple[str, list[str]]]:
+    out = []
+    for line in asm.splitlines():
+        if not line.startswith("\t") or line.lstrip().startswith((".", ";")):
+            continue
+        body = line.split(";", 1)[0].strip()
+        if not body:
+            continue
+        mnem, _, rest = body.partition(" ")
+        # operands without trailing modifiers ("s[36:37] nt" -> "s[36:37]")
+        ops = [o.split()[0] for o in rest.split(",") if o.strip()] if rest else []
+        out.append((mnem, ops))
+    return out
+
+
+def _valu_sgpr_dests(mnem: str, ops: list[str]) -> set[int]:
+    """SGPRs a VALU instruction writes: the scalar destination of readlane /
+    readfirstlane / compares, and the carry-out of *_co_* and div_scale forms."""
+    if not mnem.startswith("v_") or not ops:
+        return set()
+    dests = _sgprs(ops[0])
+    if len(ops) > 1 and ("_co_" in mnem or mnem.startswith(("v_addc", "v_subb", "v_div_scale"))):
+        dests |= _sgprs(ops[1])
+    return dests
+
+
+def hazards(asm: str) -> list[str]:
+    """Copies whose SGPR base or M0 is written too few wait states before."""
+    ins = _instructions(asm)
+    found = []
+    for j, (mnem, ops) in enumerate(ins):
+        if not mnem.startswith("global_load_lds"):
+            continue
+        base = _sgprs(ops[1]) if len(ops) > 1 else set()
+        waits = 0
+        for k in range(j - 1, -1, -1):
+            pm, pops = ins[k]
+            if pm == "s_nop":
+                waits += int(pops[0], 0) + 1
+                continue
+            if base and waits < VALU_SGPR_TO_VMEM and _valu_sgpr_dests(pm, pops) & base:
+                found.append(f"copy #{j} ({' '.join([mnem] + ops)}): base written by "
+                             f"{pm} {', '.join(pops)} {waits} wait states before")
+                break
+            if pm.startswith("s_") and pops and pops[0] == "m0" and waits < M0_TO_LDS_DMA:
+                found.append(f"copy #{j}: M0 written by {pm} {waits} wait states before")
+                break
+            waits += 1
+            if waits >= VALU_SGPR_TO_VMEM:
+                break
+    return found
+
+
+def test_checker_flags_a_stale_base():
+    """The checker itself: a base written by v_readfirstlane one instruction
+    before the copy is flagged; with s_nop 4 in between it is not."""
+    bad = ("\tv_readfirstlane_b32 s37, v15\n\tv_readfirstlane_b32 s36, v14\n"
+           "\ts_nop 0\n\tglobal_load_lds_dwordx4 v61, s[36:37] nt\n")
+    good = bad.replace("s_nop 0", "s_nop 4")
+    m0 = "\ts_mov_b32 m0, s4\n\tglobal_load_lds_dwordx4 v1, off\n"
+    assert len(hazards(bad)) == 1
+    assert hazards(good) == []
+    assert len(hazards(m0)) == 1 and hazards(m0.replace("\tglobal", "\ts_nop 0\n\tglobal")) == []
+
+
+@pytest.mark.skipif(not Path(HIPCC).exists(), reason="hipcc not available")
+def test_lds_dma_wait_states(tmp_path):
+    flags = _build_flags()
+    procs = {}
+    for src in SOURCES:
+        out = tmp_path / (src.stem + ".s")
+        procs[src.name] = (out, subprocess.Popen(
+            [HIPCC, *flags, "--cuda-device-only", "-S", "-o", str(out), str(src)],
+            stdout=subprocess.DEVNULL, stderr=subprocess.PIPE, text=True))
+    report, copies = [], 0
+    for name, (out, p) in procs.items():
+        _, err = p.communicate(timeout=600)
+        assert p.returncode == 0, f"{name}: {err[-2000:]}"
+        asm = out.read_text()
+        copies += asm.count("global_load_lds_dwordx4")
+        report += [f"{name}: {h}" for h in hazards(asm)]
+    assert copies > 0, "no LDS DMA copies found: the checker is looking at the wrong code"
+    assert not report, "\n".join(report)
