@@ -8,6 +8,8 @@ neptune_attn_fwd launch over that batch. The JSON line also carries, under
 "secondary", the split-K GQA decode (bf16 and fp8 KV) and selective-scan
 configurations measured the same way (GB/s against HBM).
 
+Each workload first runs untimed for SPINUP_S seconds (so the GPU is at its
+working clocks), then W warmup steps, then exactly K timed steps.
 roofline.achieved = algorithmic FLOPs (or bytes) per launch / mean launch
 duration from HIP events on the launch stream; cpu_baseline = the CPU oracle
 (oracle/, OpenMP) on a bounded sample of the same workload.
@@ -39,11 +41,34 @@ def prefill_flops(B, H, S, D):
     return 4.0 * B * H * D * S * (S + 1) / 2
 
 
-def time_launches(fn, steps, warmup, rotate=1):
-    """Run warmup + steps launches; returns (wall seconds for the timed
-    steps, mean per-launch seconds from HIP events on the current stream)."""
+SPINUP_S = 1.0  # untimed run of each workload before its warmup steps
+
+
+def spin_up(fn, seconds, rotate=1):
+    """Run fn, untimed, until `seconds` of wall time have passed. An idle
+    MI355X takes tens of milliseconds of load to reach its working clocks;
+    without this the first workload's timed steps run partly below them
+    (measured: ~605 us against ~555 us steady state for the prefill)."""
     import torch
 
+    t0, i = time.perf_counter(), 0
+    while True:
+        fn(i % rotate)
+        i += 1
+        if i % 8 == 0:
+            torch.cuda.synchronize()
+            if time.perf_counter() - t0 >= seconds:
+                return i
+
+
+def time_launches(fn, steps, warmup, rotate=1, spinup=SPINUP_S):
+    """Spin up, run warmup + steps launches; returns (wall seconds for the
+    timed steps, mean per-launch seconds from HIP events on the current
+    stream)."""
+    import torch
+
+    if spinup > 0:
+        spin_up(fn, spinup, rotate)
     for i in range(warmup):
         fn(i % rotate)
     torch.cuda.synchronize()
@@ -303,6 +328,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "spinup_s": SPINUP_S,
         "ms_per_step": round(res["wall"] / args.steps * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",

@@ -71,7 +71,14 @@ typedef struct neptune_backend_info {
  * Layout: Q, O [batch, heads_q, seq_q, head_dim]; K, V [batch, heads_kv,
  * seq_kv, head_dim]; the head_dim axis is contiguous. Strides are in
  * elements for the (batch, head, seq) axes; a zero stride array means
- * contiguous. Query head h reads KV head h / (heads_q / heads_kv).
+ * contiguous. With k_dim_order = 1, K is [batch, heads_kv, head_dim,
+ * seq_kv] instead (seq contiguous; k_stride gives the batch, head and
+ * head_dim-row strides): the order a dimension_order = [1, 0] tile load
+ * reads (lib/HTile/HTilePasses.cpp:122-140). pipeline_stages is the number
+ * of K and V tiles the kernel keeps in LDS per operand, i.e. how far its
+ * loads run ahead (the htile.pipeline_stages loop attribute, HTile:128);
+ * neither knob changes the result. Both apply to the head_dim-128 16-bit
+ * kernel (0 = default elsewhere); k_dim_order = 1 needs seq_kv % 8 == 0. Query head h reads KV head h / (heads_q / heads_kv).
  * Numerics follow tests/data/flash_attention_htile.mlir:23-143: scores are
  * scaled by scale_log2 (= log2(e)/sqrt(D) when 0, HTile:24) into the exp2
  * domain, the running max starts at -FLT_MAX, keys stream in blocks of 64,
@@ -86,7 +93,8 @@ typedef struct neptune_attn_desc {
   int32_t dtype;  /* F32, F16 or BF16 for q, k, v and o */
   int32_t causal;
   float scale_log2;
-  int32_t reserved;
+  int16_t pipeline_stages; /* 0 = default (2), or 1, 2, 3               */
+  int16_t k_dim_order;     /* 0: K [.., seq, head_dim]; 1: [.., head_dim, seq] */
 } neptune_attn_desc;
 
 /* Split-K decode with grouped KV heads (one query token per sequence).

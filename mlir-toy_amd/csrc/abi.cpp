@@ -161,18 +161,27 @@ neptune_status neptune_attn_fwd(const neptune_attn_desc *d, const void *q, const
                 (int)d->dtype);
   if (!(d->scale_log2 >= 0.0f) || !std::isfinite(d->scale_log2))
     return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "attn_fwd: scale_log2 must be finite and >= 0");
+  if (d->pipeline_stages < 0 || d->pipeline_stages > 3)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "attn_fwd: pipeline_stages %d (need 0..3)",
+                (int)d->pipeline_stages);
+  if (d->k_dim_order != 0 && d->k_dim_order != 1)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "attn_fwd: k_dim_order %d (need 0 or 1)",
+                (int)d->k_dim_order);
   AttnLaunch L;
   L.q = q; L.k = k; L.v = v; L.o = o; L.lse = lse;
   L.batch = d->batch; L.heads_q = d->heads_q; L.heads_kv = d->heads_kv;
   L.seq_q = d->seq_q; L.seq_kv = d->seq_kv; L.head_dim = d->head_dim;
   if (!resolve_strides(d->q_stride, d->heads_q, d->seq_q, d->head_dim, L.qs) ||
-      !resolve_strides(d->k_stride, d->heads_kv, d->seq_kv, d->head_dim, L.ks) ||
+      !(d->k_dim_order ? resolve_strides(d->k_stride, d->heads_kv, d->head_dim, d->seq_kv, L.ks)
+                       : resolve_strides(d->k_stride, d->heads_kv, d->seq_kv, d->head_dim, L.ks)) ||
       !resolve_strides(d->v_stride, d->heads_kv, d->seq_kv, d->head_dim, L.vs) ||
       !resolve_strides(d->o_stride, d->heads_q, d->seq_q, d->head_dim, L.os))
     return fail(NEPTUNE_ERR_INVALID_ARGUMENT,
                 "attn_fwd: strides must be all zero (contiguous) or all positive");
   L.dtype = d->dtype;
   L.causal = d->causal ? 1 : 0;
+  L.stages = d->pipeline_stages ? d->pipeline_stages : 2;
+  L.k_dim_order = d->k_dim_order;
   L.scale_log2 = d->scale_log2 != 0.0f
                      ? d->scale_log2
                      : (float)(1.4426950408889634 / std::sqrt((double)d->head_dim));

@@ -16,7 +16,10 @@ struct AttnArgs {
   float scale2;                             // log2(e)/sqrt(D) unless given
 };
 
-// Launches the head_dim-128 16-bit kernel (attn_fwd_d128.hip); dtype 1 = f16, 2 = bf16.
-hipError_t launch_attn_d128(const AttnArgs &a, int32_t dtype, bool causal, hipStream_t s);
+// Launches the head_dim-128 16-bit kernel (attn_fwd_d128.hip); dtype 1 = f16,
+// 2 = bf16; stages = LDS slots per operand (1, 2 or 3); kt = K stored
+// [.., head_dim, seq] (ks2 is then the head_dim-row stride).
+hipError_t launch_attn_d128(const AttnArgs &a, int32_t dtype, bool causal, int stages, bool kt,
+                            hipStream_t s);
 
 }  // namespace neptune

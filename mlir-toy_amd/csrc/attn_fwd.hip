@@ -353,6 +353,21 @@ bool attn_supported(const AttnLaunch &a, const char **why) {
     *why = "16-bit attention supports head_dim 64 or 128";
     return false;
   }
+  const bool d128 = a.dtype != 0 && a.head_dim == 128;
+  if (a.stages != 2 && !d128) {
+    *why = "pipeline_stages other than 2 applies to the head_dim-128 16-bit kernel";
+    return false;
+  }
+  if (a.k_dim_order != 0) {
+    if (!d128) {
+      *why = "k_dim_order 1 applies to the head_dim-128 16-bit kernel";
+      return false;
+    }
+    if (a.seq_kv % 8) {
+      *why = "k_dim_order 1 needs seq_kv to be a multiple of 8";
+      return false;
+    }
+  }
   if (a.seq_q > (int64_t)1 << 30 || a.seq_kv > (int64_t)1 << 30 ||
       a.batch * a.heads_q > (int64_t)1 << 24) {
     *why = "sequence or batch*heads too large for one launch";
@@ -396,7 +411,7 @@ hipError_t launch_attn_fwd(const AttnLaunch &L, hipStream_t s) {
       if (bf16) launch_mfma<Bf16Tag, 64>(a, causal, grid, s);
       else launch_mfma<F16Tag, 64>(a, causal, grid, s);
     } else {
-      return launch_attn_d128(a, L.dtype, causal, s);
+      return launch_attn_d128(a, L.dtype, causal, L.stages, L.k_dim_order != 0, s);
     }
   }
   return hipGetLastError();

@@ -24,6 +24,17 @@
 //   K: unit u of row r at u ^ (r & 15)   (reads: 32 rows, one unit each)
 //   V: unit u of row r at u ^ 4(r & 3)   (transpose reads: 4 rows x 64 B)
 //
+// Knobs (template parameters, chosen per launch):
+//   STAGES (pipeline_stages, HTile:128): K and V tiles each have STAGES LDS
+//     slots and the loads run that many key blocks ahead of their use. 2 is
+//     the default; 3 takes 96 KiB of LDS (one work-group per CU); 1 loads
+//     each tile only once the previous one has been consumed.
+//   KT (the K load order): false reads K stored [.., seq, head_dim] as key
+//     rows (the A operand of S^T = K.Q^T directly); true reads K stored
+//     [.., head_dim, seq] -- the layout a dimension_order = [1, 0] load
+//     produces (HTilePasses.cpp:122-140) -- as head_dim rows of 64 keys, and
+//     forms the A operand with ds_read_b64_tr_b16 as V^T is formed.
+//
 // Work-groups: each runs two query blocks of one head, q0 = nqb-1-p and
 // q1 = p, back to back; the K/V stream simply continues from q0's last key
 // block into q1's first, so q1's tiles (and its Q^T) load while q0 drains.
@@ -92,6 +103,49 @@ __device__ inline void tile_to_lds(const TileLoader &t, int key0, int Sk, const 
   }
 }
 
+// K stored [.., head_dim, seq]: a tile is 128 head_dim rows x 64 keys
+// (128 B). Wave w copies rows [32w, 32w+32) as four 1 KiB chunks of eight
+// rows; 16-byte unit u (keys 8u .. 8u+7) of row r sits at unit
+// u ^ 4((r >> 1) & 1), which keeps the transpose reads (four rows x 64 B
+// per 16 lanes) on distinct banks. Needs seq % 8 == 0: a unit past the end
+// of the keys re-reads the last unit (its scores are masked).
+struct KtLoader {
+  const char *base;   // element (0, 0) of this (batch, head)
+  int64_t row_bytes;  // head_dim-row stride in bytes
+  uint32_t off[4];    // per-lane byte offset of chunk c within a full block
+  int unit[4];        // source unit (keys 8 unit ..) of chunk c
+};
+
+__device__ inline KtLoader make_kt_loader(const uint16_t *src, int64_t stride, int w, int lane) {
+  KtLoader t;
+  t.base = (const char *)src;
+  t.row_bytes = stride * 2;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int r = 32 * w + 8 * c + (lane >> 3);
+    t.unit[c] = (lane & 7) ^ (((r >> 1) & 1) << 2);
+    t.off[c] = (uint32_t)((int64_t)r * t.row_bytes + t.unit[c] * 16);
+  }
+  return t;
+}
+
+__device__ inline void kt_tile_to_lds(const KtLoader &t, int key0, int Sk, const uint8_t *tile,
+                                      int w, int lane) {
+  if (key0 + BN <= Sk) {
+    const char *blk = t.base + (int64_t)key0 * 2;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) dma16(blk, t.off[c], lds_offset(tile + (4 * w + c) * 1024));
+  } else {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int r = 32 * w + 8 * c + (lane >> 3);
+      const int k8 = min(key0 + 8 * t.unit[c], Sk - 8);
+      dma16(t.base + (int64_t)r * t.row_bytes + (int64_t)k8 * 2,
+            lds_offset(tile + (4 * w + c) * 1024));
+    }
+  }
+}
+
 __device__ inline void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }  // vmcnt(0)
 
 // (lane, lane ^ 32) pair reductions through v_permlane32_swap
@@ -123,12 +177,15 @@ __device__ inline void map_block(const AttnArgs &a, int npair, int id, int *pair
   }
 }
 
-template <class E, bool CAUSAL>
-__global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a, int npair) {
+template <class E, bool CAUSAL, int STAGES, bool KT>
+__global__ __launch_bounds__(NT, STAGES == 3 ? 1 : 2) void attn_fwd_d128(AttnArgs a, int npair) {
   typedef typename E::vec8 V8;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[4 * TILE];  // K0 K1 V0 V1
+  // K slots 0 .. STAGES-1, then V slots 0 .. STAGES-1; block t uses slot t % STAGES
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGES * TILE];
   const uint8_t *const kt0 = smem;
-  const uint8_t *const vt0 = smem + 2 * TILE;
+  const uint8_t *const vt0 = smem + STAGES * TILE;
+  auto kslot = [&](int t) { return kt0 + (t % STAGES) * TILE; };
+  auto vslot = [&](int t) { return vt0 + (t % STAGES) * TILE; };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -162,23 +219,42 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a, int npair) {
   const int nv = n0 + nkb[1];  // virtual key blocks: n0 for q0, then q1's
 
   const TileLoader kl = make_loader<false>(kp, a.ks2, w, lane);
+  const KtLoader ktl = make_kt_loader(kp, a.ks2, w, lane);
   const TileLoader vl = make_loader<true>(vp, a.vs2, w, lane);
-  // virtual block t -> key block of its query block; K/V slot t & 1
+  // virtual block t -> key block of its query block
   auto vkey0 = [&](int t) { return (t < n0 ? t : t - n0) * BN; };
-  if (nv > 0) {
-    tile_to_lds<false>(kl, vkey0(0), a.Sk, kt0, w);
-    tile_to_lds<true>(vl, vkey0(0), a.Sk, vt0, w);
-    if (nv > 1) tile_to_lds<false>(kl, vkey0(1), a.Sk, kt0 + TILE, w);
-  }
+  auto load_k = [&](int t) {
+    if constexpr (KT)
+      kt_tile_to_lds(ktl, vkey0(t), a.Sk, kslot(t), w, lane);
+    else
+      tile_to_lds<false>(kl, vkey0(t), a.Sk, kslot(t), w);
+  };
+  auto load_v = [&](int t) { tile_to_lds<true>(vl, vkey0(t), a.Sk, vslot(t), w); };
+  // K of blocks 0 .. STAGES-1 and V of blocks 0 .. STAGES-2 (0 when STAGES = 1)
+#pragma unroll
+  for (int t = 0; t < STAGES; ++t)
+    if (t < nv) load_k(t);
+#pragma unroll
+  for (int t = 0; t < (STAGES > 1 ? STAGES - 1 : 1); ++t)
+    if (t < nv) load_v(t);
 
   // Q^T operand: k-step st covers head_dim 16 st + 8 g .. +7 of the row
+  // (KT: 16 st + 4 g .. +3 and 16 st + 8 + 4 g .. +3, the order in which the
+  // K^T transpose reads deliver head_dim)
   u32x4 qf[8];
   auto load_q = [&](int qb) {
     const int row = qb * BM + w * 32 + lq;
+    const uint16_t *qr = qp + row * a.qs2;
 #pragma unroll
-    for (int st = 0; st < 8; ++st)
-      qf[st] = row < a.Sq ? *(const u32x4 *)(qp + row * a.qs2 + 16 * st + 8 * g)
-                          : u32x4{0, 0, 0, 0};
+    for (int st = 0; st < 8; ++st) {
+      if constexpr (KT) {
+        const u32x2 lo = row < a.Sq ? *(const u32x2 *)(qr + 16 * st + 4 * g) : u32x2{0, 0};
+        const u32x2 hi = row < a.Sq ? *(const u32x2 *)(qr + 16 * st + 8 + 4 * g) : u32x2{0, 0};
+        qf[st] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      } else {
+        qf[st] = row < a.Sq ? *(const u32x4 *)(qr + 16 * st + 8 * g) : u32x4{0, 0, 0, 0};
+      }
+    }
   };
   load_q(qbs[0]);
 
@@ -186,9 +262,13 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a, int npair) {
   int ka[8];  // K: row lq (+32 kb), logical unit 2 st + g
 #pragma unroll
   for (int st = 0; st < 8; ++st) ka[st] = lq * 256 + (((2 * st + g) ^ (lq & 15)) << 4);
-  int va[4];  // V^T: transpose read, rows 4 g + i (+16 c + 8 t), columns 32 nb + 16 dh + 4 q
+  int kta[2];  // K^T: transpose read, rows 4 g + i (+16 st + 8 t), keys 32 kb + 16 h + 4 q
+  int va[4];   // V^T: transpose read, rows 4 g + i (+16 c + 8 t), columns 32 nb + 16 dh + 4 q
   {
     const int s16 = lane & 15, i = s16 >> 2, q = s16 & 3, dh = (lane >> 4) & 1;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+      kta[kb] = (4 * g + i) * 128 + 64 * (kb ^ (i >> 1)) + 32 * dh + 8 * q;
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) va[nb] = (4 * g + i) * 256 + 64 * (nb ^ i) + 32 * dh + 8 * q;
   }
@@ -209,21 +289,44 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a, int npair) {
   const f32x16 zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
   auto qk = [&](const uint8_t *kt) {
+    if constexpr (KT) {
 #pragma unroll
-    for (int st = 0; st < 8; ++st)
+      for (int st = 0; st < 8; ++st)
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const u32x4 A = *(const u32x4 *)(kt + kb * 8192 + ka[st]);
-        s[kb] = E::mfma32(as_vec8<V8>(A), as_vec8<V8>(qf[st]), st == 0 ? zero16 : s[kb]);
+        for (int kb = 0; kb < 2; ++kb) {
+          const v4i16 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_v4i16 *)as_lds(kt + (16 * st) * 128 + kta[kb]));
+          const v4i16 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_v4i16 *)as_lds(kt + (16 * st + 8) * 128 + kta[kb]));
+          const u32x2 a0 = __builtin_bit_cast(u32x2, t0), a1 = __builtin_bit_cast(u32x2, t1);
+          const u32x4 A = {a0[0], a0[1], a1[0], a1[1]};
+          s[kb] = E::mfma32(as_vec8<V8>(A), as_vec8<V8>(qf[st]), st == 0 ? zero16 : s[kb]);
+        }
+      // two transpose reads per MFMA, issued two MFMAs ahead
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+#pragma unroll
+      for (int i = 0; i < 14; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
       }
-    // operand reads run two MFMAs ahead (bounds the live registers)
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
+    } else {
 #pragma unroll
-    for (int i = 0; i < 14; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      for (int st = 0; st < 8; ++st)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const u32x4 A = *(const u32x4 *)(kt + kb * 8192 + ka[st]);
+          s[kb] = E::mfma32(as_vec8<V8>(A), as_vec8<V8>(qf[st]), st == 0 ? zero16 : s[kb]);
+        }
+      // operand reads run two MFMAs ahead (bounds the live registers)
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+#pragma unroll
+      for (int i = 0; i < 14; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
   };
 
   // O = acc / l rounded to the input type (HTile:130-143) and the LSE
@@ -249,14 +352,28 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a, int npair) {
 
   wait_vmem();
   __syncthreads();
-  if (nkw[0] > 0) qk(kt0);
+  if (nkw[0] > 0) qk(kslot(0));
   __syncthreads();  // every wave is done with K slot 0 before it is refilled
 
   for (int vb = 0; vb < nv; ++vb) {
     const int item = vb >= n0 ? 1 : 0;
     const int jb = vb - item * n0;  // key block within the query block
-    if (vb + 2 < nv) tile_to_lds<false>(kl, vkey0(vb + 2), a.Sk, kt0 + (vb & 1) * TILE, w);
-    if (vb + 1 < nv) tile_to_lds<true>(vl, vkey0(vb + 1), a.Sk, vt0 + ((vb + 1) & 1) * TILE, w);
+    // K of block vb + STAGES goes to the slot block vb's K has left, V of
+    // block vb + STAGES - 1 to the slot of block vb - 1's V (STAGES = 1:
+    // only K here, V once this block's P.V is done)
+    int issued = 0;
+    if constexpr (STAGES > 1) {
+      if (vb + STAGES < nv) {
+        load_k(vb + STAGES);
+        ++issued;
+      }
+      if (vb + STAGES - 1 < nv) {
+        load_v(vb + STAGES - 1);
+        ++issued;
+      }
+    } else {
+      if (vb + 1 < nv) load_k(vb + 1);
+    }
     const int qrow0 = qbs[item] * BM + w * 32;
     if (jb < nkw[item]) {
       const int key0 = jb * BN;
@@ -313,7 +430,7 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a, int npair) {
       // wave raises its issue priority for its MFMA stretch so the matrix
       // core is fed first while the other wave on the SIMD runs its softmax.
       __builtin_amdgcn_s_setprio(1);
-      const uint8_t *vt = vt0 + (vb & 1) * TILE;
+      const uint8_t *vt = vslot(vb);
 #pragma unroll
       for (int step = 0; step < 16; ++step) {
         const int c = step >> 2, nb = step & 3;
@@ -336,10 +453,28 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a, int npair) {
 
       // S^T of the next block of this query block (its K tile arrived
       // during the previous iteration)
-      if (jb + 1 < nkw[item]) qk(kt0 + ((vb + 1) & 1) * TILE);
+      if constexpr (STAGES > 1)
+        if (jb + 1 < nkw[item]) qk(kslot(vb + 1));
       __builtin_amdgcn_s_setprio(0);
     }
-    wait_vmem();
+    if constexpr (STAGES == 1) {
+      wait_vmem();
+      __syncthreads();  // K of block vb + 1 has landed; every wave is done with V
+      if (vb + 1 < nv) load_v(vb + 1);
+      if (jb + 1 < nkw[item]) qk(kslot(vb + 1));
+      wait_vmem();
+    } else if constexpr (STAGES == 3) {
+      // the tiles issued in this iteration may stay in flight (four copies
+      // per tile per wave); those issued before it are needed next
+      if (issued == 2)
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(8));
+      else if (issued == 1)
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(4));
+      else
+        wait_vmem();
+    } else {
+      wait_vmem();
+    }
     __syncthreads();
     if (vb == n0 - 1) {
       // switch to q1 (its first K tile has landed): load its Q^T here, not
@@ -352,7 +487,7 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a, int npair) {
         load_q(qbs[1]);
         wait_vmem();
       }
-      if (nkw[1] > 0) qk(kt0 + ((vb + 1) & 1) * TILE);
+      if (nkw[1] > 0) qk(kslot(vb + 1));
       __syncthreads();  // that K slot is refilled by the next iteration
     }
   }
@@ -360,23 +495,42 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_d128(AttnArgs a, int npair) {
   if (two) finalize(qbs[1]);
 }
 
-template <class E>
+template <class E, int STAGES, bool KT>
 void launch_t(const AttnArgs &a, bool causal, hipStream_t s) {
   const int npair = (a.nqb + 1) / 2;
   const dim3 grid((unsigned)(npair * a.BH));
   if (causal)
-    hipLaunchKernelGGL((attn_fwd_d128<E, true>), grid, dim3(NT), 0, s, a, npair);
+    hipLaunchKernelGGL((attn_fwd_d128<E, true, STAGES, KT>), grid, dim3(NT), 0, s, a, npair);
   else
-    hipLaunchKernelGGL((attn_fwd_d128<E, false>), grid, dim3(NT), 0, s, a, npair);
+    hipLaunchKernelGGL((attn_fwd_d128<E, false, STAGES, KT>), grid, dim3(NT), 0, s, a, npair);
+}
+
+template <class E, bool KT>
+void launch_stages(const AttnArgs &a, bool causal, int stages, hipStream_t s) {
+  if (stages == 1)
+    launch_t<E, 1, KT>(a, causal, s);
+  else if (stages == 3)
+    launch_t<E, 3, KT>(a, causal, s);
+  else
+    launch_t<E, 2, KT>(a, causal, s);
+}
+
+template <class E>
+void launch_e(const AttnArgs &a, bool causal, int stages, bool kt, hipStream_t s) {
+  if (kt)
+    launch_stages<E, true>(a, causal, stages, s);
+  else
+    launch_stages<E, false>(a, causal, stages, s);
 }
 
 }  // namespace
 
-hipError_t launch_attn_d128(const AttnArgs &a, int32_t dtype, bool causal, hipStream_t s) {
+hipError_t launch_attn_d128(const AttnArgs &a, int32_t dtype, bool causal, int stages, bool kt,
+                            hipStream_t s) {
   if (dtype == 2)
-    launch_t<Bf16Tag>(a, causal, s);
+    launch_e<Bf16Tag>(a, causal, stages, kt, s);
   else
-    launch_t<F16Tag>(a, causal, s);
+    launch_e<F16Tag>(a, causal, stages, kt, s);
   return hipGetLastError();
 }
 

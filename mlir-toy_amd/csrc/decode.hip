@@ -108,13 +108,27 @@ __global__ __launch_bounds__(RT) void decode_partial_ring(DecArgs a) {
                                                  : (int64_t)bk * a.L * DH * 2);
   const char *vbase = (const char *)a.v + (PAGED ? (int64_t)hk * a.v_ps[1] * 2
                                                  : (int64_t)bk * a.L * DH * 2);
+  // paged: 64 block-table entries of this wave's range held in a register,
+  // lane j holding entry tab0 + j, so a step takes its page with one
+  // v_readlane instead of a dependent memory load; reloaded every 64 pages
+  int tab0 = 0, tabv = 0;
+  auto load_tab = [&](int first) {
+    tab0 = first;
+    const int j = first + lane;
+    tabv = j < a.maxp ? a.btab[(int64_t)b * a.maxp + j] : 0;
+  };
   // bytes from kbase / vbase to the first row of the 32-token step at tb: a
   // step never straddles a page (the page size is a multiple of 32 and steps
   // start on multiples of 32); a block-table entry outside [0, npages) is
   // clamped so that a bad table cannot address memory outside the pages
   auto step_base = [&](int tb, int64_t *kb, int64_t *vb) {
     if (PAGED) {
-      int pg = a.btab[(int64_t)b * a.maxp + tb / a.ps];
+      const int pi = tb / a.ps;
+      if (pi - tab0 >= 64) {
+        load_tab(pi);
+        settle(tabv);
+      }
+      int pg = __builtin_amdgcn_readlane(tabv, pi - tab0);
       pg = min(max(pg, 0), a.npages - 1);
       const int64_t in_page = (int64_t)(tb % a.ps) * tokb;
       *kb = (int64_t)pg * a.k_ps[0] * 2 + in_page;
@@ -159,9 +173,6 @@ __global__ __launch_bounds__(RT) void decode_partial_ring(DecArgs a) {
       }
     }
   };
-  if (nsteps > 0) issue(0);
-  if (nsteps > 1) issue(1);
-
   // Q^T operand: k-step ks covers head_dim 32 ks + 8 G .. +7 of head n
   u32x4 qf[4];
   {
@@ -170,6 +181,13 @@ __global__ __launch_bounds__(RT) void decode_partial_ring(DecArgs a) {
     for (int ks = 0; ks < 4; ++ks)
       qf[ks] = n < Gq ? *(const u32x4 *)(qrow + 32 * ks + 8 * G) : u32x4{0, 0, 0, 0};
   }
+  if (PAGED) load_tab(t0 / a.ps);
+  // Q and the table land before the first copy is issued
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) settle(qf[ks]);
+  if (PAGED) settle(tabv);
+  if (nsteps > 0) issue(0);
+  if (nsteps > 1) issue(1);
   // LDS read offsets: K A-operand (row n of each 16-key half, unit 4 ks + G),
   // V^T transpose reads (rows 4 G + i, columns 16 mb + 4 q)
   int ka[4];
@@ -316,7 +334,7 @@ constexpr int R8W = 1;                      // waves per work-group (LDS-bound o
 constexpr int R8T = 64 * R8W;
 constexpr int R8TILE = RSTEP * DH;          // bytes of one K or V code tile
 constexpr int R8SLOT = 2 * R8TILE;
-constexpr int R8NS = 2;                     // ring slots: 1 step in flight
+constexpr int R8NS = 2;                     // ring slots: steps in flight during a step's math
 constexpr int R8WAVE = R8NS * R8SLOT;
 constexpr int R8LDS = R8W * R8WAVE;
 
@@ -372,10 +390,6 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
       }
     }
   };
-#pragma unroll
-  for (int i = 0; i < R8NS - 1; ++i)
-    if (i < nsteps) issue(i);
-
   // Q^T operand: k-step ks covers head_dim 64 (ks >> 1) + 16 G + 8 (ks & 1) .. +7
   u32x4 qf[4];
   {
@@ -386,6 +400,26 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
       qf[ks] = n < Gq ? *(const u32x4 *)(qrow + d) : u32x4{0, 0, 0, 0};
     }
   }
+  // the K / V scales of 64 scale blocks of this wave's range in registers,
+  // lane j holding block blk0 + j: a step takes its scales with v_readlane
+  // instead of a memory load; reloaded every 64 blocks
+  int blk0 = 0;
+  float kscv = 0.0f, vscv = 0.0f;
+  auto load_scales = [&](int first) {
+    blk0 = first;
+    const int j = first + lane;
+    kscv = j < a.nsb ? a.ksc[(int64_t)bk * a.nsb + j] : 0.0f;
+    vscv = j < a.nsb ? a.vsc[(int64_t)bk * a.nsb + j] : 0.0f;
+  };
+  load_scales(t0 / a.sb);
+  // Q and the scales land before the first copy is issued
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) settle(qf[ks]);
+  settle(kscv);
+  settle(vscv);
+#pragma unroll
+  for (int i = 0; i < R8NS; ++i)
+    if (i < nsteps) issue(i);
   // K reads: row n (+16 kb), logical unit 4 sp + G
   int ka[2];
 #pragma unroll
@@ -404,8 +438,8 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
 
   for (int i = 0; i < nsteps; ++i) {
     // this step's 8 copies have landed once only the later steps' may be
-    // outstanding
-    const int later = min(R8NS - 2, nsteps - 1 - i);
+    // outstanding (the next R8NS - 1 steps stay in flight during the math)
+    const int later = min(R8NS - 1, nsteps - 1 - i);
     if (later >= 2)
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(16));
     else if (later == 1)
@@ -433,8 +467,15 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
       }
     }
     const int blk = t / a.sb;
-    const float sc = a.scale2 * a.ksc[(int64_t)bk * a.nsb + blk];
-    const float vsc = a.vsc[(int64_t)bk * a.nsb + blk];
+    if (blk - blk0 >= 64) {
+      load_scales(blk);
+      settle(kscv);
+      settle(vscv);
+    }
+    const float sc = a.scale2 * __builtin_bit_cast(
+        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, kscv), blk - blk0));
+    const float vsc = __builtin_bit_cast(
+        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, vscv), blk - blk0));
     // scale first, then mask: a zero fp8 scale must not meet -inf
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -487,7 +528,7 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
       oacc[mb] = Bf16Tag::mfma16(as_vec8<bf16x8>(A), as_vec8<bf16x8>(pf), oacc[mb]);
     }
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-    if (i + R8NS - 1 < nsteps) issue(i + R8NS - 1);
+    if (i + R8NS < nsteps) issue(i + R8NS);
   }
 
   lsum += __shfl_xor(lsum, 16, 64);

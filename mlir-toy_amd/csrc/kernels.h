@@ -16,6 +16,8 @@ struct AttnLaunch {
   int32_t dtype;
   int32_t causal;
   float scale_log2;
+  int32_t stages;       // LDS slots per K/V operand (1, 2, 3)
+  int32_t k_dim_order;  // 1: K is [batch, head, head_dim, seq]; ks[2] = head_dim-row stride
 };
 
 struct DecodeLaunch {

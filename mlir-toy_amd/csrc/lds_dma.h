@@ -78,6 +78,17 @@ __device__ inline void dma16(const char *addr, uint32_t lds_addr) {
                  : "memory");
 }
 
+// Makes the compiler wait, here, for the loads that produced x (an empty
+// statement that reads x). The compiler does not count the copies above, so
+// a loop that streams through them must enter with none of the compiler's
+// own loads outstanding: a load still pending at the loop head (or issued
+// in the loop) gets a vmcnt(0) inside the loop, which also retires every
+// copy in flight and so drains the prefetch at each step.
+template <typename T>
+__device__ inline void settle(const T &x) {
+  asm volatile("" ::"v"(x));
+}
+
 // s_waitcnt immediates (gfx9 encoding): wait until at most n vector-memory
 // operations are outstanding / until all LDS operations have completed.
 constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }

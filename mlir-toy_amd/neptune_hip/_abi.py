@@ -72,7 +72,8 @@ class AttnDesc(ctypes.Structure):
         ("dtype", ctypes.c_int32),
         ("causal", ctypes.c_int32),
         ("scale_log2", ctypes.c_float),
-        ("reserved", ctypes.c_int32),
+        ("pipeline_stages", ctypes.c_int16),
+        ("k_dim_order", ctypes.c_int16),
     ]
 
 

@@ -598,9 +598,10 @@ class AttentionProgram:
     grid: tuple[int, int, int]            # (x = query block, y = head, z = batch)
     threads: tuple[int, int, int]
     scale_log2: float                     # score scale in the exp2 domain
-    pipeline_stages: int | None           # htile.pipeline_stages hint
+    pipeline_stages: int | None           # htile.pipeline_stages (bound to the kernel)
     k_dimension_order: tuple[int, int]    # (1, 0): K tile loaded transposed
     neg_init: float                       # running-max initial value
+    k_dim_order: int = 0                  # K memref: 0 = [B, H, S, D], 1 = [B, H, D, S]
 
 
 def _recognize(func: Op) -> AttentionProgram:
@@ -609,11 +610,15 @@ def _recognize(func: Op) -> AttentionProgram:
     if len(args) != 4:
         _fail(f"{name} takes {len(args)} arguments, expected q, k, v, out")
     mshapes = [shaped(t) for t in func.types]
-    if any(s != mshapes[0] for s in mshapes):
-        _fail("q, k, v and out memrefs must share one shape and element type")
+    if any(s != mshapes[0] for s in (mshapes[2], mshapes[3])):
+        _fail("q, v and out memrefs must share one shape and element type")
     shape, dtype = mshapes[0]
     if len(shape) != 4 or dtype not in ("f16", "bf16", "f32"):
         _fail(f"memref<{shape}x{dtype}> is not [B, H, S, D] in f16/bf16/f32")
+    kshape, kdtype = mshapes[1]
+    kt_shape = [shape[0], shape[1], shape[3], shape[2]]
+    if kdtype != dtype or (kshape != shape and kshape != kt_shape):
+        _fail("the k memref must be [B, H, S, D] or [B, H, D, S] of the q element type")
     q, k, v, out = args
 
     env: dict[str, object] = {q: ("arg", "q"), k: ("arg", "k"), v: ("arg", "v"), out: ("arg", "out")}
@@ -744,25 +749,35 @@ def _recognize(func: Op) -> AttentionProgram:
     block_m, dq = qt[3]
     if dq != D:
         _fail("the q tile must span head_dim")
+    # K's memref stores [S, D] or [D, S]; the tile load may transpose it
+    # (dimension_order [1, 0]) and the dot may transpose its operand: QK^T
+    # needs a [D, block_n] operand, i.e. an odd number of the three flips
+    # ([D, S] storage, [1, 0] load, transpose_b). When S == D the index
+    # pattern tells the storage order.
     k_order = tuple(kt[4])
-    if k_order == (1, 0):
-        dk, block_n = kt[3]
-    elif k_order == (0, 1):
-        block_n, dk = kt[3]
-    else:
+    if k_order not in ((0, 1), (1, 0)):
         _fail(f"K dimension_order {k_order}")
+    X, Y, Z = env[bx], env[by], env[bz]
+    mrow = _norm(("mul", X, block_m)) if X != 0 else 0
+    kidx = _norm(kt[2])
+    k_stored_t = kshape != shape or (kshape == kt_shape and kidx[2] == 0 and kidx[3] != 0)
+    tile_t = k_stored_t != (k_order == (1, 0))  # tile is [D, block_n]
+    if tile_t:
+        dk, block_n = kt[3]
+    else:
+        block_n, dk = kt[3]
     bnv, dv = vt[3]
     if dk != D or dv != D or bnv != block_n or tuple(vt[4]) != (0, 1):
         _fail("K and V tiles must be block_n x head_dim")
 
-    X, Y, Z = env[bx], env[by], env[bz]
-    mrow = _norm(("mul", X, block_m)) if X != 0 else 0
     jrow = _norm(("mul", ("iv",), block_n))
     if _norm(qt[2]) != (Z, Y, mrow, 0):
         _fail("q tile is not q[b, h, block_x * block_m, 0]")
-    for t in (kt, vt):
-        if _norm(t[2]) != (Z, Y, jrow, 0):
-            _fail("k/v tiles are not [b, h, j * block_n, 0]")
+    if _norm(vt[2]) != (Z, Y, jrow, 0):
+        _fail("the v tile is not v[b, h, j * block_n, 0]")
+    if kidx != ((Z, Y, 0, jrow) if k_stored_t else (Z, Y, jrow, 0)):
+        _fail("the k tile is not k[b, h, j * block_n, 0] (or k[b, h, 0, j * block_n] for a "
+              "[B, H, D, S] memref)")
 
     # the recurrence, with the loop-carried values as ("iter", i)
     ys = loop["yields"]
@@ -775,7 +790,7 @@ def _recognize(func: Op) -> AttentionProgram:
     if m_i is None:
         _fail("no running row max")
     score = None
-    qk = ("dot", qt, kt, k_order == (0, 1))
+    qk = ("dot", qt, kt, not tile_t)
     for i, y in enumerate(ys):
         if i == m_i:
             continue
@@ -823,11 +838,14 @@ def _recognize(func: Op) -> AttentionProgram:
     if smem != ("arg", "out") or _norm(sval) != _norm(want_out) or _norm(sidx) != (Z, Y, mrow, 0):
         _fail("the output is not trunc(acc / l) stored at out[b, h, block_x * block_m, 0]")
     stages = loop["attrs"].get("htile.pipeline_stages")
+    if stages is not None and int(stages) not in (1, 2, 3):
+        raise NotImplementedError(f"HTile front end: htile.pipeline_stages = {stages}: the HIP "
+                                  "kernel stages 1, 2 or 3 K/V tiles in LDS")
     return AttentionProgram(
         name=name, shape=(B, H, S, D), dtype=dtype, block_m=block_m, block_n=block_n,
         trip_count=trip, grid=grid, threads=threads, scale_log2=scale_log2,
         pipeline_stages=int(stages) if stages is not None else None,
-        k_dimension_order=k_order, neg_init=float(neg[1]))
+        k_dimension_order=k_order, neg_init=float(neg[1]), k_dim_order=int(k_stored_t))
 
 
 # ------------------------------------------------------------- binding
@@ -841,8 +859,10 @@ class HTileKernel:
     ``kernel[grid](q, k, v, out)`` computes what the program computes for that
     launch grid: program (bx, by, bz) writes rows [bx*block_m, +block_m) of
     out[bz, by] from q[bz, by] attending to keys [0, trip_count*block_n) of
-    k/v[bz, by]. Tensors are CUDA tensors of the memref shape and dtype with
-    the memref's identity (row-major) layout."""
+    k/v[bz, by]. Tensors are CUDA tensors of the memref shapes and dtype with
+    the memrefs' identity (row-major) layout; a [B, H, D, S] k memref binds
+    to the kernel's k_dim_order 1 and the loop's htile.pipeline_stages to
+    its pipeline_stages."""
 
     def __init__(self, program: AttentionProgram):
         self.program = program
@@ -865,13 +885,15 @@ class HTileKernel:
 
         prog = self.program
         want_dtype = getattr(torch, _TORCH_DTYPES[prog.dtype])
+        B, H, S, D = prog.shape
+        kshape = (B, H, D, S) if prog.k_dim_order else prog.shape
         for name, t in (("q", q), ("k", k), ("v", v), ("out", out)):
-            if tuple(t.shape) != prog.shape or t.dtype != want_dtype:
-                raise ValueError(f"{name}: expected {list(prog.shape)} {prog.dtype}, "
+            want = kshape if name == "k" else prog.shape
+            if tuple(t.shape) != want or t.dtype != want_dtype:
+                raise ValueError(f"{name}: expected {list(want)} {prog.dtype}, "
                                  f"got {list(t.shape)} {t.dtype}")
             if not t.is_contiguous():
                 raise ValueError(f"{name}: the memref layout is row-major contiguous")
-        B, H, S, D = prog.shape
         gx, gy, gz = grid
         rows, keys = gx * prog.block_m, prog.trip_count * prog.block_n
         if gz > B or gy > H or rows > S or keys > S:
@@ -879,8 +901,10 @@ class HTileKernel:
                              f"key blocks of {prog.block_n} reads outside the memrefs {prog.shape}")
         if min(grid) <= 0:
             return out
-        ops.attention(q[:gz, :gy, :rows], k[:gz, :gy, :keys], v[:gz, :gy, :keys], causal=False,
-                      out=out[:gz, :gy, :rows], scale_log2=prog.scale_log2)
+        kk = k[:gz, :gy, :, :keys] if prog.k_dim_order else k[:gz, :gy, :keys]
+        ops.attention(q[:gz, :gy, :rows], kk, v[:gz, :gy, :keys], causal=False,
+                      out=out[:gz, :gy, :rows], scale_log2=prog.scale_log2,
+                      pipeline_stages=prog.pipeline_stages or 0, k_dim_order=prog.k_dim_order)
         return out
 
 

@@ -65,6 +65,8 @@ def attention(
     out: torch.Tensor | None = None,
     lse: torch.Tensor | None = None,
     scale_log2: float | None = None,
+    pipeline_stages: int = 0,
+    k_dim_order: int = 0,
 ):
     """softmax(q k^T * scale) v with the HTile numeric policy.
 
@@ -72,6 +74,10 @@ def attention(
     returns out [B, Hq, Sq, D] (and lse [B, Hq, Sq] fp32 if asked).
     ``scale_log2`` gives the score scale already in the exp2 domain (the
     HTile program's own constant, HTile:24), in place of ``scale``.
+    ``pipeline_stages`` (0 = default 2, or 1..3) sets how many K/V tiles the
+    kernel stages in LDS ahead of use; with ``k_dim_order=1`` k is given as
+    [B, Hkv, D, Skv] (seq contiguous), the order of a dimension_order =
+    [1, 0] tile load. Neither changes the result.
     """
     if scale is not None and scale_log2 is not None:
         raise ValueError("give scale or scale_log2, not both")
@@ -79,8 +85,13 @@ def attention(
     if q.dtype not in _TORCH_TO_DTYPE or k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError(f"q, k, v must share one of {list(_TORCH_TO_DTYPE)}")
     B, Hq, Sq, D = q.shape
-    Bk, Hk, Sk, Dk = k.shape
-    if (Bk, Dk) != (B, D) or tuple(v.shape) != tuple(k.shape):
+    if k_dim_order not in (0, 1):
+        raise ValueError("k_dim_order must be 0 or 1")
+    if k_dim_order:
+        Bk, Hk, Dk, Sk = k.shape
+    else:
+        Bk, Hk, Sk, Dk = k.shape
+    if (Bk, Dk) != (B, D) or tuple(v.shape) != (Bk, Hk, Sk, Dk):
         raise ValueError(f"shape mismatch: q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
     if out is None:
         out = torch.empty_like(q, memory_format=torch.contiguous_format)
@@ -102,6 +113,8 @@ def attention(
     desc.dtype = _TORCH_TO_DTYPE[q.dtype]
     desc.causal = 1 if causal else 0
     desc.scale_log2 = float(scale_log2) if scale_log2 is not None else scale_to_log2(scale, D)
+    desc.pipeline_stages = int(pipeline_stages)
+    desc.k_dim_order = int(k_dim_order)
     lib = load_library()
     with torch.cuda.device(q.device):
         check(

@@ -41,7 +41,8 @@ class AttnDesc(ctypes.Structure):
         ("dtype", ctypes.c_int32),
         ("causal", ctypes.c_int32),
         ("scale_log2", ctypes.c_float),
-        ("reserved", ctypes.c_int32),
+        ("pipeline_stages", ctypes.c_int16),
+        ("k_dim_order", ctypes.c_int16),
     ]
 
 
@@ -166,19 +167,22 @@ def decode(bits: np.ndarray, dtype: int) -> np.ndarray:
 # -------------------------------------------------------------- attention
 
 
-def _attn_desc(q, k, dtype, causal, scale_log2) -> AttnDesc:
+def _attn_desc(q, k, dtype, causal, scale_log2, k_dim_order=0) -> AttnDesc:
     B, Hq, Sq, D = q.shape
-    _, Hk, Sk, _ = k.shape
+    Hk, Sk = k.shape[1], (k.shape[3] if k_dim_order else k.shape[2])
     d = AttnDesc()
     d.batch, d.heads_q, d.heads_kv, d.seq_q, d.seq_kv, d.head_dim = B, Hq, Hk, Sq, Sk, D
     d.dtype, d.causal, d.scale_log2 = dtype, 1 if causal else 0, scale_log2
+    d.k_dim_order = k_dim_order
     return d
 
 
-def attn_fwd(q, k, v, dtype: int, causal: bool = False, scale_log2: float = 0.0):
-    """HTile-policy attention. Returns (o storage bits, lse float32)."""
+def attn_fwd(q, k, v, dtype: int, causal: bool = False, scale_log2: float = 0.0,
+             k_dim_order: int = 0):
+    """HTile-policy attention. Returns (o storage bits, lse float32).
+    k_dim_order=1: k is given [B, Hk, D, Sk]."""
     q, k, v = (np.ascontiguousarray(t) for t in (q, k, v))
-    d = _attn_desc(q, k, dtype, causal, scale_log2)
+    d = _attn_desc(q, k, dtype, causal, scale_log2, k_dim_order)
     o = np.empty(q.shape, dtype=_NP_STORAGE[dtype])
     lse = np.empty(q.shape[:3], dtype=np.float32)
     _check(lib().neptune_cpu_attn_fwd(ctypes.byref(d), _ptr(q), _ptr(k), _ptr(v), _ptr(o),
@@ -186,10 +190,11 @@ def attn_fwd(q, k, v, dtype: int, causal: bool = False, scale_log2: float = 0.0)
     return o, lse
 
 
-def attn_exact(q, k, v, dtype: int, causal: bool = False, scale_log2: float = 0.0):
+def attn_exact(q, k, v, dtype: int, causal: bool = False, scale_log2: float = 0.0,
+               k_dim_order: int = 0):
     """fp64 closed form. Returns (o float64, lse float64)."""
     q, k, v = (np.ascontiguousarray(t) for t in (q, k, v))
-    d = _attn_desc(q, k, dtype, causal, scale_log2)
+    d = _attn_desc(q, k, dtype, causal, scale_log2, k_dim_order)
     o = np.empty(q.shape, dtype=np.float64)
     lse = np.empty(q.shape[:3], dtype=np.float64)
     _check(lib().neptune_cpu_attn_exact(ctypes.byref(d), _ptr(q), _ptr(k), _ptr(v), _ptr(o),

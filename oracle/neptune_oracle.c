@@ -201,6 +201,9 @@ static int attn_check(const neptune_attn_desc *d, const void *q, const void *k,
   if (d->dtype != NEPTUNE_DTYPE_F32 && d->dtype != NEPTUNE_DTYPE_F16 &&
       d->dtype != NEPTUNE_DTYPE_BF16)
     return NEPTUNE_ERR_INVALID_ARGUMENT;
+  if (d->pipeline_stages < 0 || d->pipeline_stages > 3 ||
+      (d->k_dim_order != 0 && d->k_dim_order != 1))
+    return NEPTUNE_ERR_INVALID_ARGUMENT;
   return NEPTUNE_OK;
 }
 
@@ -217,6 +220,21 @@ static void strides_or_contig(const int64_t in[3], int64_t heads, int64_t seq,
   }
 }
 
+/* K's (batch, head) base strides plus its token and head_dim strides:
+ * k_dim_order 0 stores K [B, Hk, S, D], 1 stores it [B, Hk, D, S]. */
+static void k_layout(const neptune_attn_desc *d, int64_t ks[3], int64_t *tok,
+                     int64_t *dim) {
+  if (d->k_dim_order) {
+    strides_or_contig(d->k_stride, d->heads_kv, d->head_dim, d->seq_kv, ks);
+    *tok = 1;
+    *dim = ks[2];
+  } else {
+    strides_or_contig(d->k_stride, d->heads_kv, d->seq_kv, d->head_dim, ks);
+    *tok = ks[2];
+    *dim = 1;
+  }
+}
+
 static float default_scale_log2(float given, int64_t dim) {
   return given != 0.0f ? given : (float)(LOG2E / sqrt((double)dim));
 }
@@ -227,7 +245,8 @@ static float default_scale_log2(float given, int64_t dim) {
 typedef struct {
   const void *k, *v;
   int32_t dt;          /* storage type of k and v */
-  int64_t kbase, vbase, kstride, vstride; /* element offsets */
+  int64_t kbase, vbase, kstride, vstride; /* element offsets; strides per token */
+  int64_t kdstride;    /* K's head_dim stride: 1, or the row stride of [.., D, S] */
   const float *kscale, *vscale; /* per token block (fp8), or NULL */
   int64_t scale_block;
   int32_t p_dtype;     /* type P is rounded to before P.V */
@@ -236,8 +255,8 @@ typedef struct {
 static inline float kv_load(const kv_view *kv, int which, int64_t t,
                             int64_t dd) {
   const void *base = which ? kv->v : kv->k;
-  int64_t off = (which ? kv->vbase : kv->kbase) +
-                t * (which ? kv->vstride : kv->kstride) + dd;
+  int64_t off = which ? kv->vbase + t * kv->vstride + dd
+                      : kv->kbase + t * kv->kstride + dd * kv->kdstride;
   float x = load_elem(base, off, kv->dt);
   const float *sc = which ? kv->vscale : kv->kscale;
   if (sc) x *= sc[t / kv->scale_block];
@@ -298,9 +317,9 @@ int32_t neptune_cpu_attn_fwd(const neptune_attn_desc *d, const void *q,
   if (!o) return NEPTUNE_ERR_INVALID_ARGUMENT;
   const int64_t B = d->batch, Hq = d->heads_q, Hk = d->heads_kv, Sq = d->seq_q,
                 Sk = d->seq_kv, D = d->head_dim, group = Hq / Hk;
-  int64_t qs[3], ks[3], vs[3], os[3];
+  int64_t qs[3], ks[3], vs[3], os[3], ktok, kdim;
   strides_or_contig(d->q_stride, Hq, Sq, D, qs);
-  strides_or_contig(d->k_stride, Hk, Sk, D, ks);
+  k_layout(d, ks, &ktok, &kdim);
   strides_or_contig(d->v_stride, Hk, Sk, D, vs);
   strides_or_contig(d->o_stride, Hq, Sq, D, os);
   const float scale2 = default_scale_log2(d->scale_log2, D);
@@ -315,8 +334,10 @@ int32_t neptune_cpu_attn_fwd(const neptune_attn_desc *d, const void *q,
         float *acc = qrow + D;
         for (int64_t dd = 0; dd < D; ++dd)
           qrow[dd] = load_elem(q, b * qs[0] + h * qs[1] + i * qs[2] + dd, dt);
-        kv_view kv = {k, v, dt, b * ks[0] + hk * ks[1], b * vs[0] + hk * vs[1],
-                      ks[2], vs[2], NULL, NULL, 1, dt};
+        kv_view kv = {.k = k, .v = v, .dt = dt, .kbase = b * ks[0] + hk * ks[1],
+                      .vbase = b * vs[0] + hk * vs[1], .kstride = ktok, .vstride = vs[2],
+                      .kdstride = kdim, .kscale = NULL, .vscale = NULL, .scale_block = 1,
+                      .p_dtype = dt};
         int64_t visible = Sk;
         if (d->causal) {
           int64_t last = i + (Sk - Sq);
@@ -346,9 +367,9 @@ int32_t neptune_cpu_attn_exact(const neptune_attn_desc *d, const void *q,
   if (!o) return NEPTUNE_ERR_INVALID_ARGUMENT;
   const int64_t B = d->batch, Hq = d->heads_q, Hk = d->heads_kv, Sq = d->seq_q,
                 Sk = d->seq_kv, D = d->head_dim, group = Hq / Hk;
-  int64_t qs[3], ks[3], vs[3], os_unused[3];
+  int64_t qs[3], ks[3], vs[3], os_unused[3], ktok, kdim;
   strides_or_contig(d->q_stride, Hq, Sq, D, qs);
-  strides_or_contig(d->k_stride, Hk, Sk, D, ks);
+  k_layout(d, ks, &ktok, &kdim);
   strides_or_contig(d->v_stride, Hk, Sk, D, vs);
   (void)os_unused;
   const double scale = (double)default_scale_log2(d->scale_log2, D) * LN2;
@@ -371,7 +392,7 @@ int32_t neptune_cpu_attn_exact(const neptune_attn_desc *d, const void *q,
           for (int64_t dd = 0; dd < D; ++dd)
             dot += (double)load_elem(q, b * qs[0] + h * qs[1] + i * qs[2] + dd,
                                      dt) *
-                   (double)load_elem(k, b * ks[0] + hk * ks[1] + j * ks[2] + dd,
+                   (double)load_elem(k, b * ks[0] + hk * ks[1] + j * ktok + dd * kdim,
                                      dt);
           s[j] = dot * scale;
           if (s[j] > mx) mx = s[j];
@@ -449,11 +470,11 @@ int32_t neptune_cpu_decode_splitk(const neptune_decode_desc *d, const void *q,
       float *qrow = buf, *ot = buf + D, *ms = ot + S * D, *ls = ms + S;
       for (int64_t dd = 0; dd < D; ++dd)
         qrow[dd] = load_elem(q, (b * Hq + h) * D + dd, d->q_dtype);
-      kv_view kv = {k, v, d->kv_dtype, (b * Hk + hk) * L * D,
-                    (b * Hk + hk) * L * D, D, D,
-                    fp8 ? k_scale + (b * Hk + hk) * nsb : NULL,
-                    fp8 ? v_scale + (b * Hk + hk) * nsb : NULL, sb,
-                    d->q_dtype};
+      kv_view kv = {.k = k, .v = v, .dt = d->kv_dtype, .kbase = (b * Hk + hk) * L * D,
+                    .vbase = (b * Hk + hk) * L * D, .kstride = D, .vstride = D,
+                    .kdstride = 1, .kscale = fp8 ? k_scale + (b * Hk + hk) * nsb : NULL,
+                    .vscale = fp8 ? v_scale + (b * Hk + hk) * nsb : NULL, .scale_block = sb,
+                    .p_dtype = d->q_dtype};
       for (int64_t s = 0; s < S; ++s) {
         int64_t k0 = s * chunk, k1 = k0 + chunk < L ? k0 + chunk : L;
         htile_row(qrow, D, &kv, k0, k1, k1, scale2, ot + s * D, &ms[s], &ls[s]);

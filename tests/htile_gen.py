@@ -8,7 +8,9 @@ htile-dot-transpose-to-load-order pass (K tile loaded with
 ``canonical=True`` values carry numbered names (``%0``, ``%c0``, ``%cst``,
 loop results as ``%r:3`` used as ``%r#i``), ops appear in another order
 and a size-1 grid dimension's block id is folded to ``%c0``, as after
-canonicalisation. ``mutate`` swaps in one wrong piece for negative tests.
+canonicalisation. ``k_mem="ds"`` declares K as [B, H, D, S] and loads its
+[D, block_n] tile in stored order (no transpose anywhere). ``mutate`` swaps
+in one wrong piece for negative tests.
 """
 
 from __future__ import annotations
@@ -20,12 +22,13 @@ ELT = {"f16": "f16", "bf16": "bf16", "f32": "f32"}
 
 def program(B=1, H=32, S=4096, D=128, dtype="f16", bm=128, bn=64, form="pre", grid=None,
             threads=128, trip=None, scale=None, stages=2, canonical=False, name="flash_attention_htile",
-            mutate=None):
+            mutate=None, k_mem="sd"):
     e = ELT[dtype]
     grid = grid or (S // bm, H, B)
     trip = trip if trip is not None else S // bn
     scale = scale if scale is not None else math.log2(math.e) / math.sqrt(D)
     mem = f"memref<{B}x{H}x{S}x{D}x{e}>"
+    kmem = f"memref<{B}x{H}x{D}x{S}x{e}>" if k_mem == "ds" else mem
     sh = "#htile.encoding<placement = shared>" if canonical else "#shared"
     lo = "#htile.encoding<placement = local>" if canonical else "#local"
 
@@ -43,7 +46,7 @@ def program(B=1, H=32, S=4096, D=128, dtype="f16", bm=128, bn=64, form="pre", gr
         L += ["#shared = #htile.encoding<placement = shared>",
               "#local = #htile.encoding<placement = local>", ""]
     L += ["module {",
-          f"  func.func @{name}(%q: {mem}, %k: {mem}, %v: {mem}, %out: {mem}) {{"]
+          f"  func.func @{name}(%q: {mem}, %k: {kmem}, %v: {mem}, %out: {mem}) {{"]
     L += ["    %c0 = arith.constant 0 : index", "    %c1 = arith.constant 1 : index"]
     sizes = sorted({grid[0], grid[1], grid[2], threads, bm, bn, trip} - {0, 1})
     for s in sizes:
@@ -74,7 +77,13 @@ def program(B=1, H=32, S=4096, D=128, dtype="f16", bm=128, bn=64, form="pre", gr
     jb, kt, qk, sc, sco, rm, mn = (v(x) for x in ("j_base", "k_tile", "qk", "scale_t", "score",
                                                   "row_max", "m_next"))
     L.append(f"        {jb} = arith.muli %j, {c(bn)} : index")
-    if form == "pre":
+    if k_mem == "ds":
+        tb = " {transpose_b, warp_policy = \"full_row\"}" if mutate == "kt_transpose" else \
+            " {warp_policy = \"full_row\"}"
+        L.append(f"        {kt} = htile.load %k[{zero_b}, %by, %c0, {jb}] : {kmem} -> {t([D, bn], e, sh)}")
+        L.append(f"        {qk} = htile.dot {qs}, {kt}{tb} : "
+                 f"{t([bm, D], e, sh)}, {t([D, bn], e, sh)} -> {t([bm, bn])}")
+    elif form == "pre":
         L.append(f"        {kt} = htile.load %k[{zero_b}, %by, {jb}, %c0] : {mem} -> {t([bn, D], e, sh)}")
         L.append(f"        {qk} = htile.dot {qs}, {kt} {{transpose_b, warp_policy = \"full_row\"}} : "
                  f"{t([bm, D], e, sh)}, {t([bn, D], e, sh)} -> {t([bm, bn])}")

@@ -81,7 +81,8 @@ int main(void) {
   F(neptune_attn_desc, seq_q) F(neptune_attn_desc, seq_kv) F(neptune_attn_desc, head_dim)
   F(neptune_attn_desc, q_stride) F(neptune_attn_desc, k_stride) F(neptune_attn_desc, v_stride)
   F(neptune_attn_desc, o_stride) F(neptune_attn_desc, dtype) F(neptune_attn_desc, causal)
-  F(neptune_attn_desc, scale_log2) F(neptune_attn_desc, reserved) S(neptune_attn_desc)
+  F(neptune_attn_desc, scale_log2) F(neptune_attn_desc, pipeline_stages)
+  F(neptune_attn_desc, k_dim_order) S(neptune_attn_desc)
   F(neptune_decode_desc, batch) F(neptune_decode_desc, heads_q) F(neptune_decode_desc, heads_kv)
   F(neptune_decode_desc, seq_kv) F(neptune_decode_desc, head_dim)
   F(neptune_decode_desc, num_splits) F(neptune_decode_desc, scale_block)
@@ -151,6 +152,9 @@ def _attn(lib, d, ptrs=(FAKE, FAKE, FAKE, FAKE)):
     ("head_dim", 96, _abi.ERR_UNSUPPORTED),
     ("scale_log2", float("nan"), _abi.ERR_INVALID_ARGUMENT),
     ("scale_log2", -1.0, _abi.ERR_INVALID_ARGUMENT),
+    ("pipeline_stages", 4, _abi.ERR_INVALID_ARGUMENT),
+    ("pipeline_stages", -1, _abi.ERR_INVALID_ARGUMENT),
+    ("k_dim_order", 2, _abi.ERR_INVALID_ARGUMENT),
 ])
 def test_attn_validation(lib, field, value, status):
     assert _attn(lib, _attn_desc(**{field: value})) == status
@@ -168,6 +172,36 @@ def test_attn_null_and_stride_errors(lib):
     assert _attn(lib, d) == _abi.ERR_UNSUPPORTED
     assert _attn(lib, _attn_desc(), (FAKE + 2, FAKE, FAKE, FAKE)) == _abi.ERR_UNSUPPORTED
     assert b"aligned" in lib.neptune_last_error()
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(pipeline_stages=3, head_dim=64), _abi.ERR_UNSUPPORTED),   # knob is head_dim-128 only
+    (dict(pipeline_stages=1, dtype=_abi.DTYPE_F32), _abi.ERR_UNSUPPORTED),
+    (dict(k_dim_order=1, head_dim=64), _abi.ERR_UNSUPPORTED),
+    (dict(k_dim_order=1, seq_kv=100), _abi.ERR_UNSUPPORTED),         # contiguous K^T row of 100
+    (dict(pipeline_stages=2, dtype=_abi.DTYPE_F32, head_dim=64), _abi.ERR_NO_DEVICE),
+    (dict(pipeline_stages=3, k_dim_order=1), _abi.ERR_NO_DEVICE),
+    (dict(pipeline_stages=1), _abi.ERR_NO_DEVICE),
+])
+def test_attn_knob_validation(lib, kw, status):
+    """Knob combinations the kernels do not cover are rejected before any
+    device call; valid ones get as far as the device check (only where no
+    device exists: these descriptors carry placeholder pointers)."""
+    if status == _abi.ERR_NO_DEVICE and lib.neptune_device_count() > 0:
+        pytest.skip("a HIP device is visible; the no-device path is not reachable")
+    assert _attn(lib, _attn_desc(**kw)) == status
+
+
+def test_attn_k_dim_order_strides(lib):
+    """With k_dim_order 1 the K strides are (batch, head, head_dim row): a
+    row stride of 260 elements passes the 16-bit rules only if it is a
+    multiple of 8."""
+    d = _attn_desc(k_dim_order=1, seq_kv=256)
+    d.k_stride[:] = (2 * 128 * 264, 128 * 264, 260)
+    assert _attn(lib, d) == _abi.ERR_UNSUPPORTED
+    if lib.neptune_device_count() == 0:
+        d.k_stride[:] = (2 * 128 * 264, 128 * 264, 264)
+        assert _attn(lib, d) == _abi.ERR_NO_DEVICE
 
 
 def _dec_desc(**kw):

@@ -5,8 +5,9 @@ The first case is the reference's own functional test through this front
 end (tests/test_translators.py:106-143 in Evan-Zhao/mlir-toy): f16
 [1, 32, 4096, 128], grid (32, 32, 1), an fp32 torch reference computed in
 128-row blocks, atol 1e-3. The others cover the post-pass program form,
-bf16 and fp32 against the oracle, and a grid / trip count that covers only
-part of the tensors.
+bf16 and fp32 against the oracle, a grid / trip count that covers only
+part of the tensors, and a program over a [B, H, D, S] k memref with its
+pipeline_stages bound to the kernel.
 """
 
 import math
@@ -103,3 +104,24 @@ def test_partial_grid_and_trip_count(htile):
                                oracle.BF16, causal=False)
     assert np.abs(got[:, :3, :256] - oracle.decode(ref_o, oracle.BF16)).max() <= TOL_BF16_ABS
     assert (got[:, :3, 256:] == 7.0).all() and (got[:, 3:] == 7.0).all()
+
+
+@pytest.mark.parametrize("stages", [1, 3])
+def test_transposed_k_program_and_stages(htile, stages):
+    """A program over a [B, H, D, S] k memref (its K tile read in stored
+    order) runs on the kernel's k_dim_order 1 path, with the loop's
+    htile.pipeline_stages bound to the kernel; a partial trip count reads
+    only the first keys of the transposed memref."""
+    _log(f"case: htile K^T memref, stages={stages}")
+    B, H, S, D = 1, 4, 512, 128
+    kern = htile.translate_source(program(B=B, H=H, S=S, D=D, dtype="bf16", k_mem="ds",
+                                          stages=stages, trip=6)).flash_attention_htile
+    assert kern.program.k_dim_order == 1 and kern.program.pipeline_stages == stages
+    q, k, v = (randn((B, H, S, D), seed=s, dtype=torch.bfloat16) for s in (12, 13, 14))
+    out = torch.empty((B, H, S, D), dtype=torch.bfloat16, device="cuda")
+    kern[kern.program.grid](q.cuda(), k.transpose(2, 3).contiguous().cuda(), v.cuda(), out)
+    torch.cuda.synchronize()
+    keys = 6 * 64
+    ref_o, _ = oracle.attn_fwd(bits(q), bits(k[:, :, :keys]), bits(v[:, :, :keys]), oracle.BF16,
+                               causal=False)
+    assert np.abs(to_f32(out) - oracle.decode(ref_o, oracle.BF16)).max() <= TOL_BF16_ABS

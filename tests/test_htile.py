@@ -56,6 +56,29 @@ def test_parameters_follow_the_program():
     assert p.scale_log2 == 0.25 and p.pipeline_stages == 3 and p.grid == (4, 3, 1)
 
 
+@pytest.mark.parametrize("canonical", [False, True])
+@pytest.mark.parametrize("S", [1024, 128])  # S == D: the index pattern tells the storage order
+def test_k_stored_transposed_binds_k_dim_order(canonical, S):
+    p = _prog(program(B=1, H=2, S=S, D=128, dtype="bf16", k_mem="ds", stages=3,
+                      canonical=canonical))
+    assert p.k_dim_order == 1 and p.k_dimension_order == (0, 1)
+    assert (p.block_n, p.trip_count, p.pipeline_stages) == (64, S // 64, 3)
+    for form in ("pre", "post"):
+        q = _prog(program(B=1, H=2, S=S, D=128, dtype="bf16", form=form, canonical=canonical))
+        assert q.k_dim_order == 0
+
+
+def test_k_stored_transposed_and_transposed_again_is_rejected():
+    # [D, S] storage, plain [D, block_n] tile, then transpose_b: that is Q.K, not Q.K^T
+    with pytest.raises(NotImplementedError, match="not a flash-attention tile program"):
+        htile.translate_source(program(S=256, H=2, k_mem="ds", mutate="kt_transpose"))
+
+
+def test_stage_counts_the_kernel_does_not_stage_are_rejected():
+    with pytest.raises(NotImplementedError, match="pipeline_stages = 4"):
+        htile.translate_source(program(S=256, H=2, stages=4))
+
+
 def test_without_pipeline_hint():
     assert _prog(program(S=256, H=2, stages=None)).pipeline_stages is None
 
@@ -87,6 +110,15 @@ def test_launch_checks_run_before_the_device():
         kern[(4, 2, 1)](t, t, t, t)
     with pytest.raises(ValueError, match="device tensors"):
         kern[(2, 2, 1)](t, t, t, t)
+
+
+def test_launch_checks_the_transposed_k_shape():
+    torch = pytest.importorskip("torch")
+    kern = htile.translate_source(program(B=1, H=2, S=256, D=128, dtype="bf16",
+                                          k_mem="ds")).flash_attention_htile
+    t = torch.zeros((1, 2, 256, 128), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match=r"k: expected \[1, 2, 128, 256\]"):
+        kern(t, t, t, t)
 
 
 def test_cli_prints_the_binding(tmp_path, capsys):

@@ -194,6 +194,28 @@ def test_attn_shift_and_permutation_invariance():
     assert np.abs(permuted - base).max() < 1e-12
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_attn_k_dim_order_is_layout_only(causal):
+    """K given [B, Hk, D, Sk] with k_dim_order 1 is the same operand as
+    K [B, Hk, Sk, D]: the HTile policy and the fp64 closed form give
+    identical results, and a strided K^T view (padded rows) is read in
+    place."""
+    B, Hq, Hk, Sq, Sk, D = 2, 4, 2, 40, 72, 16
+    q = bits(randn((B, Hq, Sq, D), seed=61))
+    k = bits(randn((B, Hk, Sk, D), seed=62))
+    v = bits(randn((B, Hk, Sk, D), seed=63))
+    kt = np.ascontiguousarray(k.transpose(0, 1, 3, 2))
+    o0, l0 = oracle.attn_fwd(q, k, v, oracle.BF16, causal=causal)
+    o1, l1 = oracle.attn_fwd(q, kt, v, oracle.BF16, causal=causal, k_dim_order=1)
+    assert np.array_equal(o0, o1) and np.array_equal(l0, l1)
+    e0, _ = oracle.attn_exact(q, k, v, oracle.BF16, causal=causal)
+    e1, _ = oracle.attn_exact(q, kt, v, oracle.BF16, causal=causal, k_dim_order=1)
+    assert np.array_equal(e0, e1)
+    # the same K^T buffer read in the other order is a different operand
+    o2, _ = oracle.attn_fwd(q, kt.reshape(B, Hk, Sk, D), v, oracle.BF16, causal=causal)
+    assert not np.array_equal(o0, o2)
+
+
 def test_attn_gqa_equals_repeated_mha():
     q = randn((1, 8, 40, 64), 20, torch.bfloat16)
     k = randn((1, 2, 40, 64), 21, torch.bfloat16)
