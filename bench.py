@@ -61,12 +61,13 @@ def spin_up(fn, seconds, rotate=1):
                 return i
 
 
-def time_launches(fn, steps, warmup, rotate=1, spinup=SPINUP_S):
+def time_launches(fn, steps, warmup, rotate=1, spinup=None):
     """Spin up, run warmup + steps launches; returns (wall seconds for the
     timed steps, mean per-launch seconds from HIP events on the current
     stream)."""
     import torch
 
+    spinup = SPINUP_S if spinup is None else spinup
     if spinup > 0:
         spin_up(fn, spinup, rotate)
     for i in range(warmup):
@@ -247,6 +248,7 @@ def hbm_entry(key, name, wall, ev, nbytes, steps, traffic):
 
 
 def main():
+    global SPINUP_S
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
@@ -259,7 +261,11 @@ def main():
                     help="run one configuration only (for profiling); 'copy' is a plain "
                          "1 GiB device copy used to calibrate HBM byte counters")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--spinup", type=float, default=SPINUP_S,
+                    help="untimed seconds of each workload before its warmup steps "
+                         "(0 for counter-collection runs, which need no steady clocks)")
     args = ap.parse_args()
+    SPINUP_S = args.spinup
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
