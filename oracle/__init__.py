@@ -62,6 +62,18 @@ class DecodeDesc(ctypes.Structure):
     ]
 
 
+class PagedKvDesc(ctypes.Structure):
+    """include/neptune_hip.h: neptune_paged_kv_desc"""
+
+    _fields_ = [
+        ("num_pages", ctypes.c_int64),
+        ("page_size", ctypes.c_int64),
+        ("max_pages", ctypes.c_int64),
+        ("k_stride", ctypes.c_int64 * 3),
+        ("v_stride", ctypes.c_int64 * 3),
+    ]
+
+
 class ScanDesc(ctypes.Structure):
     _fields_ = [
         ("batch", ctypes.c_int64),
@@ -115,6 +127,10 @@ def lib() -> ctypes.CDLL:
             ctypes.POINTER(DecodeDesc), vp, vp, vp, vp, vp, vp, vp, vp,
         ]
         L.neptune_cpu_decode_splitk.restype = i32
+        L.neptune_cpu_decode_paged.argtypes = [
+            ctypes.POINTER(DecodeDesc), ctypes.POINTER(PagedKvDesc), vp, vp, vp, vp, vp, vp, vp,
+        ]
+        L.neptune_cpu_decode_paged.restype = i32
         L.neptune_cpu_decode_layout.argtypes = [
             ctypes.POINTER(DecodeDesc), ctypes.POINTER(i64), ctypes.POINTER(i64),
         ]
@@ -241,6 +257,37 @@ def decode_splitk(q, k, v, kv_dtype: int = BF16, k_scale=None, v_scale=None,
                                            _ptr(k_scale), _ptr(v_scale), _ptr(o), _ptr(lse),
                                            _ptr(parts)), "decode_splitk")
     return o, lse, parts
+
+
+def decode_paged(q, k_pool, v_pool, block_table, seq_lens, max_seq_len=None,
+                 num_splits: int = 0, scale_log2: float = 0.0):
+    """Split-K decode over a paged pool. q [B,Hq,D] bf16 bits; k_pool /
+    v_pool bf16 bits viewed as [pages, Hk, page_size, D] (any element strides
+    with D contiguous; read in place); block_table [B, max_pages] and
+    seq_lens [B] int32. Returns (o bits, lse)."""
+    q = np.ascontiguousarray(q)
+    block_table = np.ascontiguousarray(block_table, dtype=np.int32)
+    seq_lens = np.ascontiguousarray(seq_lens, dtype=np.int32)
+    for pool in (k_pool, v_pool):
+        if pool.dtype != np.uint16 or pool.ndim != 4 or pool.strides[3] != 2:
+            raise ValueError("pools must be uint16 [pages, Hk, page_size, D] with D contiguous")
+    npages, Hk, ps, D = k_pool.shape
+    L = int(max_seq_len) if max_seq_len is not None else block_table.shape[1] * ps
+    d = DecodeDesc()
+    d.batch, d.heads_q, d.heads_kv, d.seq_kv, d.head_dim = q.shape[0], q.shape[1], Hk, L, D
+    d.num_splits, d.scale_block = num_splits, 64
+    d.q_dtype, d.kv_dtype, d.scale_log2 = BF16, BF16, scale_log2
+    pk = PagedKvDesc()
+    pk.num_pages, pk.page_size, pk.max_pages = npages, ps, block_table.shape[1]
+    pk.k_stride[:] = tuple(x // 2 for x in k_pool.strides[:3])
+    pk.v_stride[:] = tuple(x // 2 for x in v_pool.strides[:3])
+    o = np.empty(q.shape, dtype=np.uint16)
+    lse = np.empty(q.shape[:2], dtype=np.float32)
+    _check(lib().neptune_cpu_decode_paged(ctypes.byref(d), ctypes.byref(pk), _ptr(q),
+                                          k_pool.ctypes.data, v_pool.ctypes.data,
+                                          _ptr(block_table), _ptr(seq_lens), _ptr(o), _ptr(lse)),
+           "decode_paged")
+    return o, lse
 
 
 def kv_quantize_fp8(src_bits: np.ndarray, scale_block: int = 64):

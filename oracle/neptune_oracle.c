@@ -250,13 +250,25 @@ typedef struct {
   const float *kscale, *vscale; /* per token block (fp8), or NULL */
   int64_t scale_block;
   int32_t p_dtype;     /* type P is rounded to before P.V */
+  /* paged KV (btab != NULL): token t lives in page btab[t / page_size]
+   * (clamped to [0, num_pages)), at that page's base (page strides kpage /
+   * vpage) plus kbase / vbase, row t % page_size */
+  const int32_t *btab;
+  int64_t page_size, num_pages, kpage, vpage;
 } kv_view;
 
 static inline float kv_load(const kv_view *kv, int which, int64_t t,
                             int64_t dd) {
   const void *base = which ? kv->v : kv->k;
-  int64_t off = which ? kv->vbase + t * kv->vstride + dd
-                      : kv->kbase + t * kv->kstride + dd * kv->kdstride;
+  int64_t row = t, page_off = 0;
+  if (kv->btab) {
+    int64_t pg = kv->btab[t / kv->page_size];
+    pg = pg < 0 ? 0 : (pg >= kv->num_pages ? kv->num_pages - 1 : pg);
+    page_off = pg * (which ? kv->vpage : kv->kpage);
+    row = t % kv->page_size;
+  }
+  int64_t off = which ? page_off + kv->vbase + row * kv->vstride + dd
+                      : page_off + kv->kbase + row * kv->kstride + dd * kv->kdstride;
   float x = load_elem(base, off, kv->dt);
   const float *sc = which ? kv->vscale : kv->kscale;
   if (sc) x *= sc[t / kv->scale_block];
@@ -495,6 +507,66 @@ int32_t neptune_cpu_decode_splitk(const neptune_decode_desc *d, const void *q,
         store_elem(o, (b * Hq + h) * D + dd, d->q_dtype, acc / Lsum);
       }
       if (lse) lse[b * Hq + h] = (M + log2f(Lsum)) * (float)LN2;
+      free(buf);
+    }
+  return NEPTUNE_OK;
+}
+
+/* Split-K decode over a paged KV pool: the same split layout (from
+ * seq_kv, the longest sequence) and the same per-split recurrence and
+ * combine as neptune_cpu_decode_splitk, with sequence b's tokens read
+ * through its block-table row and only its first seq_lens[b] tokens (clamped
+ * to [0, seq_kv]) visible. An empty sequence gives O = 0 and lse = -inf. */
+int32_t neptune_cpu_decode_paged(const neptune_decode_desc *d,
+                                 const neptune_paged_kv_desc *pk, const void *q,
+                                 const void *k_pages, const void *v_pages,
+                                 const int32_t *block_table,
+                                 const int32_t *seq_lens, void *o, float *lse) {
+  if (!d || !pk || !q || !k_pages || !v_pages || !block_table || !seq_lens || !o)
+    return NEPTUNE_ERR_INVALID_ARGUMENT;
+  if (d->heads_q <= 0 || d->heads_kv <= 0 || d->heads_q % d->heads_kv ||
+      d->head_dim <= 0 || d->kv_dtype != NEPTUNE_DTYPE_BF16)
+    return NEPTUNE_ERR_INVALID_ARGUMENT;
+  if (pk->num_pages <= 0 || pk->page_size <= 0 || pk->max_pages <= 0 ||
+      pk->max_pages * pk->page_size < d->seq_kv)
+    return NEPTUNE_ERR_INVALID_ARGUMENT;
+  int64_t S, chunk;
+  int st = neptune_cpu_decode_layout(d, &S, &chunk);
+  if (st) return st;
+  const int64_t B = d->batch, Hq = d->heads_q, Hk = d->heads_kv,
+                L = d->seq_kv, D = d->head_dim, group = Hq / Hk;
+  const float scale2 = default_scale_log2(d->scale_log2, D);
+
+#pragma omp parallel for collapse(2) schedule(dynamic, 1)
+  for (int64_t b = 0; b < B; ++b)
+    for (int64_t h = 0; h < Hq; ++h) {
+      int64_t hk = h / group;
+      int64_t len = seq_lens[b] < 0 ? 0 : (seq_lens[b] > L ? L : seq_lens[b]);
+      float *buf = (float *)malloc(sizeof(float) * (size_t)(D * (S + 1) + 2 * S));
+      float *qrow = buf, *ot = buf + D, *ms = ot + S * D, *ls = ms + S;
+      for (int64_t dd = 0; dd < D; ++dd)
+        qrow[dd] = load_elem(q, (b * Hq + h) * D + dd, d->q_dtype);
+      kv_view kv = {.k = k_pages, .v = v_pages, .dt = d->kv_dtype,
+                    .kbase = hk * pk->k_stride[1], .vbase = hk * pk->v_stride[1],
+                    .kstride = pk->k_stride[2], .vstride = pk->v_stride[2], .kdstride = 1,
+                    .kscale = NULL, .vscale = NULL, .scale_block = 1, .p_dtype = d->q_dtype,
+                    .btab = block_table + b * pk->max_pages, .page_size = pk->page_size,
+                    .num_pages = pk->num_pages, .kpage = pk->k_stride[0],
+                    .vpage = pk->v_stride[0]};
+      for (int64_t s = 0; s < S; ++s) {
+        int64_t k0 = s * chunk, k1 = k0 + chunk < len ? k0 + chunk : len;
+        htile_row(qrow, D, &kv, k0, k1, k1, scale2, ot + s * D, &ms[s], &ls[s]);
+      }
+      float M = -FLT_MAX;
+      for (int64_t s = 0; s < S; ++s) M = ms[s] > M ? ms[s] : M;
+      float Lsum = 0.0f;
+      for (int64_t s = 0; s < S; ++s) Lsum += exp2f(ms[s] - M) * ls[s];
+      for (int64_t dd = 0; dd < D; ++dd) {
+        float acc = 0.0f;
+        for (int64_t s = 0; s < S; ++s) acc += exp2f(ms[s] - M) * ot[s * D + dd];
+        store_elem(o, (b * Hq + h) * D + dd, d->q_dtype, Lsum > 0.0f ? acc / Lsum : 0.0f);
+      }
+      if (lse) lse[b * Hq + h] = Lsum > 0.0f ? (M + log2f(Lsum)) * (float)LN2 : -INFINITY;
       free(buf);
     }
   return NEPTUNE_OK;

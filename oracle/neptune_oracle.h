@@ -20,6 +20,10 @@
  *   decode_splitk   attn_exact with seq_q = 1; splits=1 == splits=k; GQA ==
  *                   MHA with repeated KV heads; fp8 == bf16 run on the
  *                   dequantised values
+ *   decode_paged    == decode_splitk bit for bit over a shuffled pool (both
+ *                   page layouts) at full lengths; ragged lengths against
+ *                   attn_exact on each sequence's own tokens; empty sequence
+ *                   and out-of-pool table entries
  *   kv_quantize     codes decode to within half an E4M3 ulp of x/scale,
  *                   scale = amax/448, block amax maps to code 0x7e
  *   selective_scan  brute-force numpy recurrence on tiny inputs; delta -> 0,
@@ -67,6 +71,13 @@ int32_t neptune_cpu_decode_splitk(const neptune_decode_desc *d, const void *q,
                                   const void *k, const void *v,
                                   const float *k_scale, const float *v_scale,
                                   void *o, float *lse, float *partials);
+
+/* split-K decode over a paged KV pool (neptune_decode_paged's twin) */
+int32_t neptune_cpu_decode_paged(const neptune_decode_desc *d,
+                                 const neptune_paged_kv_desc *pk, const void *q,
+                                 const void *k_pages, const void *v_pages,
+                                 const int32_t *block_table,
+                                 const int32_t *seq_lens, void *o, float *lse);
 
 /* number of splits and tokens per split the decode path uses */
 int32_t neptune_cpu_decode_layout(const neptune_decode_desc *d,

@@ -118,7 +118,7 @@ def test_ctypes_descriptors_match_the_c_header(tmp_path):
     pairs = [("neptune_attn_desc", _abi.AttnDesc, oracle.AttnDesc),
              ("neptune_decode_desc", _abi.DecodeDesc, oracle.DecodeDesc),
              ("neptune_scan_desc", _abi.ScanDesc, oracle.ScanDesc),
-             ("neptune_paged_kv_desc", _abi.PagedKvDesc, None),
+             ("neptune_paged_kv_desc", _abi.PagedKvDesc, oracle.PagedKvDesc),
              ("neptune_backend_info", _abi.BackendInfo, None)]
     for cname, prod, orc in pairs:
         for cls in (prod, orc):

@@ -4,9 +4,10 @@
   pool equals contiguous decode of the same tokens bit for bit (same kernel
   arithmetic, only the addressing differs), for both pool layouts
   ([pages, Hkv, page, D] and [pages, page, Hkv, D] seen through a view).
-* Ragged lengths: each sequence against the oracle on its own tokens.
+* Ragged lengths: each sequence against the oracle on its own tokens, and
+  the whole batch against the oracle's paged twin (same split layout).
 * A zero-length sequence gives O = 0 and lse = -inf; block-table entries
-  outside the pool are clamped by the kernel (finite output, no fault).
+  outside the pool are clamped by the kernel exactly as by the twin.
 """
 
 import numpy as np
@@ -85,6 +86,10 @@ def test_paged_ragged_lengths_match_oracle(ops):
                               torch.tensor(lens, dtype=torch.int32, device="cuda"),
                               max_seq_len=L, num_splits=4, return_lse=True)
     torch.cuda.synchronize()
+    to, tl = oracle.decode_paged(bits(q), bits(kp), bits(vp), table.cpu().numpy(),
+                                 np.array(lens, np.int32), max_seq_len=L, num_splits=4)
+    assert np.abs(to_f32(o) - oracle.decode(to, oracle.BF16)).max() <= TOL_BF16_ABS
+    assert np.abs(to_f32(lse) - tl).max() <= TOL_LSE_ABS
     for b, n in enumerate(lens):
         ro, rl, _ = oracle.decode_splitk(bits(q[b:b + 1]), bits(k[b:b + 1, :, :n]),
                                          bits(v[b:b + 1, :, :n]), oracle.BF16, num_splits=1)
@@ -112,3 +117,6 @@ def test_paged_empty_sequence_and_bad_table(ops):
     o2 = ops.decode_paged(q, kp, vp, bad, lens, max_seq_len=L)
     torch.cuda.synchronize()
     assert torch.isfinite(o2.float()).all()
+    to, _ = oracle.decode_paged(bits(q), bits(kp), bits(vp), bad.cpu().numpy(),
+                                lens.cpu().numpy(), max_seq_len=L)
+    assert np.abs(to_f32(o2) - oracle.decode(to, oracle.BF16)).max() <= TOL_BF16_ABS

@@ -286,6 +286,70 @@ def test_decode_split_invariance_and_gqa():
     assert np.array_equal(o16, om)
 
 
+def _paginate(kv, ps, rng, token_major=False, spare=3):
+    """Scatter bits [B, Hk, L, D] into a shuffled pool; returns the pool as a
+    [pages, Hk, ps, D] view and the block table."""
+    B, Hk, L, D = kv.shape
+    per = -(-L // ps)
+    npages = B * per + spare
+    ids = rng.permutation(npages)[: B * per].reshape(B, per).astype(np.int32)
+    pool = np.zeros((npages, ps, Hk, D) if token_major else (npages, Hk, ps, D), np.uint16)
+    for b in range(B):
+        for j in range(per):
+            blk = kv[b, :, j * ps:(j + 1) * ps]
+            if token_major:
+                pool[ids[b, j], :blk.shape[1]] = blk.transpose(1, 0, 2)
+            else:
+                pool[ids[b, j], :, :blk.shape[1]] = blk
+    return (pool.transpose(0, 2, 1, 3) if token_major else pool), ids
+
+
+@pytest.mark.parametrize("token_major", [False, True])
+def test_decode_paged_equals_contiguous(token_major):
+    """At full lengths the paged twin reads the same tokens in the same split
+    layout as the contiguous decode: bit-identical output and lse."""
+    rng = np.random.default_rng(5)
+    B, Hq, Hk, L, D, ps = 2, 8, 2, 640, 32, 64
+    q = bits(randn((B, Hq, D), seed=50))
+    k, v = bits(randn((B, Hk, L, D), seed=51)), bits(randn((B, Hk, L, D), seed=52))
+    kp, tab = _paginate(k, ps, np.random.default_rng(7), token_major)
+    vp, _ = _paginate(v, ps, np.random.default_rng(7), token_major)
+    lens = np.full(B, L, np.int32)
+    o0, l0, _ = oracle.decode_splitk(q, k, v, oracle.BF16, num_splits=3)
+    o1, l1 = oracle.decode_paged(q, kp, vp, tab, lens, max_seq_len=L, num_splits=3)
+    assert np.array_equal(o0, o1) and np.array_equal(l0, l1)
+    # a table that points one page elsewhere changes the result
+    bad = tab.copy()
+    bad[0, 1] = tab[1, 1]
+    o2, _ = oracle.decode_paged(q, kp, vp, bad, lens, max_seq_len=L, num_splits=3)
+    assert not np.array_equal(o0, o2)
+
+
+def test_decode_paged_ragged_empty_and_clamped():
+    B, Hq, Hk, L, D, ps = 3, 4, 2, 256, 32, 64
+    q = bits(randn((B, Hq, D), seed=53))
+    k, v = bits(randn((B, Hk, L, D), seed=54)), bits(randn((B, Hk, L, D), seed=55))
+    kp, tab = _paginate(k, ps, np.random.default_rng(8))
+    vp, _ = _paginate(v, ps, np.random.default_rng(8))
+    lens = np.array([200, 0, 37], np.int32)
+    o, lse = oracle.decode_paged(q, kp, vp, tab, lens, max_seq_len=L, num_splits=2)
+    for b, n in ((0, 200), (2, 37)):
+        ex, exl = oracle.attn_exact(q[b][None, :, None], k[b][None, :, :n], v[b][None, :, :n],
+                                    oracle.BF16)
+        got = oracle.decode(o[b], oracle.BF16)
+        assert np.abs(got - ex[0, :, 0]).max() <= 1e-2 * np.abs(ex).max()
+        assert np.abs(lse[b] - exl[0, :, 0]).max() <= 1e-3
+    assert (oracle.decode(o[1], oracle.BF16) == 0).all() and np.isneginf(lse[1]).all()
+    # entries outside the pool read the nearest page of the pool, as the kernel does
+    bad = tab.copy()
+    bad[2, 0] = -7
+    o2, _ = oracle.decode_paged(q, kp, vp, bad, lens, max_seq_len=L, num_splits=2)
+    fix = tab.copy()
+    fix[2, 0] = 0
+    o3, _ = oracle.decode_paged(q, kp, vp, fix, lens, max_seq_len=L, num_splits=2)
+    assert np.array_equal(o2, o3)
+
+
 def test_decode_fp8_equals_dequantised_exact():
     q = randn((2, 8, 128), 60)
     k = randn((2, 2, 640, 128), 61)
