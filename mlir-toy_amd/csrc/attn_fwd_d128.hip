@@ -6,21 +6,23 @@
 // head_dim 128 in bf16 or f16.
 //
 // Work-group: 256 threads = 4 waves, 128 query rows (32 per wave), 64-key
-// blocks; two work-groups per CU. Each wave forms the transposed products
+// blocks; two work-groups per CU (one with 3 stages). Each wave forms the
+// transposed products
 //   S^T = K . Q^T   (A = K rows from LDS, B = Q^T in VGPRs)
 //   O^T = V^T . P^T (A = V^T from LDS via ds_read_b64_tr_b16, B = P^T)
 // with v_mfma_f32_32x32x16, so a lane owns one query row in both
 // accumulators (row max/sum are in-lane plus one v_permlane32_swap).
 //
 // Data movement: K and V tiles go HBM -> LDS with global_load_lds_dwordx4
-// (no VGPR staging), double-buffered per operand. Key block j+1's QK^T is
-// issued in the same MFMA stream as block j's PV, so the next scores are
-// ready when the softmax of the next iteration starts, and the loads for
-// blocks j+2 (K) and j+1 (V) are in flight during iteration j.
+// (no VGPR staging) into STAGES slots per operand (default 2). Key block
+// j+1's QK^T is issued in the same MFMA stream as block j's PV, so the next
+// scores are ready when the softmax of the next iteration starts; with two
+// stages the loads for blocks j+2 (K) and j+1 (V) are in flight during
+// iteration j.
 //
-// LDS tiles are 64 rows x 256 B of 16-byte units, XOR-swizzled per row so
-// that both the DMA writes (16 lanes = one row) and the MFMA operand reads
-// are bank-conflict free:
+// LDS tiles (K stored [.., seq, head_dim], and V) are 64 rows x 256 B of
+// 16-byte units, XOR-swizzled per row so that both the DMA writes (16 lanes
+// = one row) and the MFMA operand reads are bank-conflict free:
 //   K: unit u of row r at u ^ (r & 15)   (reads: 32 rows, one unit each)
 //   V: unit u of row r at u ^ 4(r & 3)   (transpose reads: 4 rows x 64 B)
 //

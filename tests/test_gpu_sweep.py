@@ -1,0 +1,189 @@
+"""Seeded random-shape sweeps of every GPU entry point against the oracle.
+
+Each case draws its shape, layout and options from a fixed seed (so a
+failure names a reproducible case), prints them before the GPU call and
+checks the result against the CPU oracle at the contract's tolerances:
+
+* prefill (neptune_attn_fwd): batch, heads, GQA group, ragged Sq and Sk
+  (including Sq > Sk under the causal mask, where early rows see no key),
+  head_dim 64 / 128, bf16 / f16, the pipeline_stages and k_dim_order
+  knobs, and strided views of larger buffers;
+* split-K decode (neptune_decode_splitk): bf16 and fp8 KV, GQA groups 1-16,
+  ragged L, explicit and library-chosen split counts, fp8 scale blocks of
+  32, 64 and 128 tokens;
+* paged decode (neptune_decode_paged): page sizes 32-256, both pool
+  layouts, ragged lengths including empty sequences.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import (TOL_BF16_ABS, TOL_FP8_ABS, TOL_LSE_ABS, bits, max_abs, oracle_dtype,
+                     randn, to_f32)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ops():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    from neptune_hip import ops as _ops
+    return _ops
+
+
+def _log(msg):
+    print(msg, flush=True)
+
+
+def _lse_close(got, ref):
+    """Equal -inf pattern (rows that see no key), finite values within tolerance."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref))
+    fin = np.isfinite(ref)
+    assert np.isfinite(got[fin]).all()
+    if fin.any():
+        assert np.abs(got[fin] - ref[fin]).max() <= TOL_LSE_ABS
+
+
+def _prefill_case(i):
+    rng = np.random.default_rng(1000 + i)
+    D = int(rng.choice([64, 128, 128]))
+    B = int(rng.integers(1, 3))
+    Hk = int(rng.choice([1, 2, 4]))
+    Hq = Hk * int(rng.choice([1, 2, 4]))
+    Sq = int(rng.integers(1, 700))
+    Sk = int(rng.integers(1, 900))
+    causal = bool(rng.integers(0, 2))
+    dtype = torch.bfloat16 if rng.integers(0, 2) else torch.float16
+    stages = int(rng.choice([0, 1, 2, 3])) if D == 128 else 0
+    kd = int(D == 128 and Sk % 8 == 0 and rng.integers(0, 2))
+    strided = bool(rng.integers(0, 2))
+    return dict(B=B, Hq=Hq, Hk=Hk, Sq=Sq, Sk=Sk, D=D, causal=causal, dtype=dtype,
+                stages=stages, kd=kd, strided=strided, seed=1000 + i)
+
+
+@pytest.mark.parametrize("i", range(24))
+def test_prefill_sweep(ops, i):
+    c = _prefill_case(i)
+    _log(f"case: prefill sweep {c}")
+    B, Hq, Hk, Sq, Sk, D = c["B"], c["Hq"], c["Hk"], c["Sq"], c["Sk"], c["D"]
+    q = randn((B, Hq, Sq, D), seed=c["seed"], dtype=c["dtype"])
+    k = randn((B, Hk, Sk, D), seed=c["seed"] + 1, dtype=c["dtype"])
+    v = randn((B, Hk, Sk, D), seed=c["seed"] + 2, dtype=c["dtype"])
+    ro, rl = oracle.attn_fwd(bits(q), bits(k), bits(v), oracle_dtype(q), c["causal"])
+    ref = oracle.decode(ro, oracle_dtype(q))
+    kk = k.transpose(2, 3) if c["kd"] else k
+    if c["strided"]:
+        # every tensor a view into a larger buffer (padded head_dim rows / seq)
+        def pad(t, last_pad):
+            buf = torch.zeros(t.shape[:-1] + (t.shape[-1] + last_pad,), dtype=t.dtype)
+            buf[..., :t.shape[-1]] = t
+            return buf.cuda()[..., :t.shape[-1]]
+        qd, vd = pad(q, 8), pad(v, 16)
+        if c["kd"]:
+            kbuf = torch.zeros(kk.shape[:-1] + (kk.shape[-1] + 8,), dtype=kk.dtype)
+            kbuf[..., :kk.shape[-1]] = kk
+            kdv = kbuf.cuda()[..., :kk.shape[-1]]
+        else:
+            kdv = pad(kk, 24)
+    else:
+        qd, kdv, vd = q.cuda(), kk.contiguous().cuda(), v.cuda()
+    o, lse = ops.attention(qd, kdv, vd, causal=c["causal"], return_lse=True,
+                           pipeline_stages=c["stages"], k_dim_order=c["kd"])
+    torch.cuda.synchronize()
+    assert max_abs(to_f32(o), ref) <= TOL_BF16_ABS
+    _lse_close(to_f32(lse), rl)
+
+
+def _decode_case(i):
+    rng = np.random.default_rng(2000 + i)
+    B = int(rng.integers(1, 5))
+    Hk = int(rng.choice([1, 2, 4, 8]))
+    group = int(rng.choice([1, 2, 4, 8, 16]))
+    L = int(rng.integers(1, 3000))
+    splits = int(rng.choice([0, 1, 3, 7]))
+    fp8 = bool(rng.integers(0, 2))
+    sb = int(rng.choice([32, 64, 128]))
+    return dict(B=B, Hq=Hk * group, Hk=Hk, L=L, splits=splits, fp8=fp8, sb=sb, seed=2000 + i)
+
+
+@pytest.mark.parametrize("i", range(16))
+def test_decode_sweep(ops, i):
+    c = _decode_case(i)
+    _log(f"case: decode sweep {c}")
+    B, Hq, Hk, L = c["B"], c["Hq"], c["Hk"], c["L"]
+    q = randn((B, Hq, 128), seed=c["seed"])
+    k = randn((B, Hk, L, 128), seed=c["seed"] + 1)
+    v = randn((B, Hk, L, 128), seed=c["seed"] + 2)
+    if c["fp8"]:
+        kc, ks = ops.kv_quantize_fp8(k.cuda(), scale_block=c["sb"])
+        vc, vs = ops.kv_quantize_fp8(v.cuda(), scale_block=c["sb"])
+        o, lse = ops.decode_splitk(q.cuda(), kc, vc, k_scale=ks, v_scale=vs,
+                                   num_splits=c["splits"], scale_block=c["sb"], return_lse=True)
+        torch.cuda.synchronize()
+        ro, rl, _ = oracle.decode_splitk(bits(q), kc.cpu().numpy(), vc.cpu().numpy(), oracle.FP8,
+                                         ks.cpu().numpy(), vs.cpu().numpy(),
+                                         num_splits=c["splits"], scale_block=c["sb"])
+        tol = TOL_FP8_ABS
+    else:
+        o, lse = ops.decode_splitk(q.cuda(), k.cuda(), v.cuda(), num_splits=c["splits"],
+                                   return_lse=True)
+        torch.cuda.synchronize()
+        ro, rl, _ = oracle.decode_splitk(bits(q), bits(k), bits(v), oracle.BF16,
+                                         num_splits=c["splits"])
+        tol = TOL_BF16_ABS
+    ref = oracle.decode(ro, oracle.BF16)
+    err = max_abs(to_f32(o), ref)
+    assert err <= tol and err <= tol * np.abs(ref).max()
+    assert max_abs(to_f32(lse), rl) <= TOL_LSE_ABS
+
+
+def _paginate(kv, ps, rng, token_major):
+    B, Hk, L, D = kv.shape
+    per = -(-L // ps)
+    npages = B * per + 2
+    ids = torch.from_numpy(rng.permutation(npages)[: B * per].reshape(B, per).astype(np.int32))
+    shape = (npages, ps, Hk, D) if token_major else (npages, Hk, ps, D)
+    pool = torch.zeros(shape, dtype=kv.dtype)
+    for b in range(B):
+        for j in range(per):
+            blk = kv[b, :, j * ps:(j + 1) * ps]
+            if token_major:
+                pool[ids[b, j], :blk.shape[1]] = blk.transpose(0, 1)
+            else:
+                pool[ids[b, j], :, :blk.shape[1]] = blk
+    view = pool.cuda()
+    return (view.permute(0, 2, 1, 3) if token_major else view), ids.cuda()
+
+
+@pytest.mark.parametrize("i", range(8))
+def test_paged_decode_sweep(ops, i):
+    rng = np.random.default_rng(3000 + i)
+    B = int(rng.integers(1, 4))
+    Hk = int(rng.choice([1, 2, 4]))
+    Hq = Hk * int(rng.choice([1, 4, 8]))
+    ps = int(rng.choice([32, 64, 128, 256]))
+    L = int(rng.integers(ps, 2500))
+    lens = [int(x) for x in rng.integers(0, L + 1, size=B)]
+    token_major = bool(rng.integers(0, 2))
+    splits = int(rng.choice([0, 2, 5]))
+    _log(f"case: paged sweep B={B} Hq={Hq} Hk={Hk} page={ps} L={L} lens={lens} "
+         f"token_major={token_major} splits={splits}")
+    q = randn((B, Hq, 128), seed=3000 + i)
+    k = randn((B, Hk, L, 128), seed=3100 + i)
+    v = randn((B, Hk, L, 128), seed=3200 + i)
+    kp, table = _paginate(k, ps, np.random.default_rng(3300 + i), token_major)
+    vp, _ = _paginate(v, ps, np.random.default_rng(3300 + i), token_major)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    o, lse = ops.decode_paged(q.cuda(), kp, vp, table, sl.cuda(), max_seq_len=L,
+                              num_splits=splits, return_lse=True)
+    torch.cuda.synchronize()
+    ro, rl = oracle.decode_paged(bits(q), bits(kp), bits(vp), table.cpu().numpy(), sl.numpy(),
+                                 max_seq_len=L, num_splits=splits)
+    ref = oracle.decode(ro, oracle.BF16)
+    assert max_abs(to_f32(o), ref) <= TOL_BF16_ABS
+    _lse_close(to_f32(lse), rl)
