@@ -767,24 +767,21 @@ hipError_t launch_decode(const DecodeLaunch &L, hipStream_t s) {
   a.v_ps[0] = L.v_pstride[0];
   a.v_ps[1] = L.v_pstride[1];
   const int grid = (int)(L.batch * L.heads_kv * L.splits);
+  // Each kernel's dynamic-LDS limit is set once per process (function-local
+  // statics are initialised exactly once, also under concurrent first calls);
+  // a failure is kept and returned by every later launch.
   if (L.kv_dtype == 3) {
-    static bool attr8_set = false;  // benign race: the attribute is idempotent
-    if (!attr8_set) {
-      hipError_t e = hipFuncSetAttribute((const void *)decode_partial_ring8,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, R8LDS);
-      if (e != hipSuccess) return e;
-      attr8_set = true;
-    }
+    static const hipError_t attr8 = hipFuncSetAttribute(
+        (const void *)decode_partial_ring8, hipFuncAttributeMaxDynamicSharedMemorySize, R8LDS);
+    if (attr8 != hipSuccess) return attr8;
     hipLaunchKernelGGL(decode_partial_ring8, dim3(grid), dim3(R8T), R8LDS, s, a);
   } else {
-    static bool attr_set[2] = {false, false};  // benign race: the attribute is idempotent
-    const void *fn = paged ? (const void *)decode_partial_ring<true>
-                           : (const void *)decode_partial_ring<false>;
-    if (!attr_set[paged]) {
-      hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, RLDS);
-      if (e != hipSuccess) return e;
-      attr_set[paged] = true;
-    }
+    static const hipError_t attr_c = hipFuncSetAttribute(
+        (const void *)decode_partial_ring<false>, hipFuncAttributeMaxDynamicSharedMemorySize, RLDS);
+    static const hipError_t attr_p = hipFuncSetAttribute(
+        (const void *)decode_partial_ring<true>, hipFuncAttributeMaxDynamicSharedMemorySize, RLDS);
+    const hipError_t attr = paged ? attr_p : attr_c;
+    if (attr != hipSuccess) return attr;
     if (paged)
       hipLaunchKernelGGL(decode_partial_ring<true>, dim3(grid), dim3(RT), RLDS, s, a);
     else
