@@ -239,8 +239,7 @@ __global__ __launch_bounds__(RT) void decode_partial_ring(DecArgs a) {
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kb][r]);
-    mx = wave_max_xor(mx, 16);
-    mx = wave_max_xor(mx, 32);
+    mx = max_xor32(max_xor16(mx));
     // lazy rescale: the running max moves only past a 2^kSlack margin
     if (__any(mx > m + kSlack)) {
       const float m_new = fmaxf(m, mx);
@@ -412,6 +411,9 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
     vscv = j < a.nsb ? a.vsc[(int64_t)bk * a.nsb + j] : 0.0f;
   };
   load_scales(t0 / a.sb);
+  // scale block of the current step, kept by counting (a step is 32 tokens
+  // and a block a multiple of 32, so steps never straddle blocks)
+  int blk = t0 / a.sb, in_blk = t0 - blk * a.sb;
   // Q and the scales land before the first copy is issued
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) settle(qf[ks]);
@@ -466,7 +468,6 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
         }
       }
     }
-    const int blk = t / a.sb;
     if (blk - blk0 >= 64) {
       load_scales(blk);
       settle(kscv);
@@ -493,8 +494,7 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kb][r]);
-    mx = wave_max_xor(mx, 16);
-    mx = wave_max_xor(mx, 32);
+    mx = max_xor32(max_xor16(mx));
     // lazy rescale: the running max moves only past a 2^kSlack margin
     if (__any(mx > m + kSlack)) {
       const float m_new = fmaxf(m, mx);
@@ -529,6 +529,11 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
     }
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
     if (i + R8NS < nsteps) issue(i + R8NS);
+    in_blk += RSTEP;
+    if (in_blk == a.sb) {
+      in_blk = 0;
+      ++blk;
+    }
   }
 
   lsum += __shfl_xor(lsum, 16, 64);

@@ -80,8 +80,18 @@ __device__ inline float swap_halves(float x) {
   return __shfl_xor(x, 32, 64);
 }
 
-__device__ inline float wave_max_xor(float x, int mask) {
-  return fmaxf(x, __shfl_xor(x, mask, 64));
+// max(x, x of lane l ^ 16) and max(x, x of lane l ^ 32), in registers: with
+// both operands x, v_permlane16_swap exchanges rows 0 <-> 1 and 2 <-> 3 (16
+// lanes each) and v_permlane32_swap the two 32-lane halves, so one of the
+// two results is x and the other its partner, with no LDS round trip (what
+// __shfl_xor's ds_bpermute costs)
+__device__ inline float max_xor16(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float max_xor32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // OCP E4M3FN -> f32 for two codes (hardware, exact): bytes 0,1 (HI=false)
