@@ -381,13 +381,16 @@ __global__ __launch_bounds__(NT, STAGES == 3 ? 1 : 2) void attn_fwd_d128(AttnArg
       const int key0 = jb * BN;
       const bool need_mask = (key0 + BN > a.Sk) || (CAUSAL && key0 + BN - 1 > qrow0 + a.off);
       if (need_mask) {
+        // element (kb, r) holds key key0 + 4 g + c with c = 32 kb + 8 (r >> 2)
+        // + (r & 3), a constant: it is masked when c passes the lane's last
+        // visible key (the sequence end or, causally, the lane's own row)
+        int lim = a.Sk - 1 - key0 - 4 * g;
+        if (CAUSAL) lim = min(lim, qrow0 + lq + a.off - key0 - 4 * g);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = key0 + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3);
-            if (key >= a.Sk || (CAUSAL && key > qrow0 + lq + a.off)) s[kb][r] = -INFINITY;
-          }
+          for (int r = 0; r < 16; ++r)
+            if (32 * kb + 8 * (r >> 2) + (r & 3) > lim) s[kb][r] = -INFINITY;
       }
       float mx = -INFINITY;
 #pragma unroll
