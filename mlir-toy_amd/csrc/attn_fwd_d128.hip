@@ -93,7 +93,7 @@ __device__ inline void tile_to_lds(const TileLoader &t, int key0, int Sk, const 
   if (key0 + BN <= Sk) {
     const char *blk = t.base + (int64_t)key0 * t.row_bytes;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) dma16(blk, t.off[c], lds_offset(tile + (4 * w + c) * 1024));
+    for (int c = 0; c < 4; ++c) dma16_sbase(blk, t.off[c], lds_offset(tile + (4 * w + c) * 1024));
   } else {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -136,7 +136,7 @@ __device__ inline void kt_tile_to_lds(const KtLoader &t, int key0, int Sk, const
   if (key0 + BN <= Sk) {
     const char *blk = t.base + (int64_t)key0 * 2;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) dma16(blk, t.off[c], lds_offset(tile + (4 * w + c) * 1024));
+    for (int c = 0; c < 4; ++c) dma16_sbase(blk, t.off[c], lds_offset(tile + (4 * w + c) * 1024));
   } else {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {

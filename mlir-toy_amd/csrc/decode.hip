@@ -153,9 +153,20 @@ __global__ __launch_bounds__(RT) void decode_partial_ring(DecArgs a) {
     if (tb + RSTEP <= Lb) {
       const char *kb = kbase + kb0, *vb = vbase + vb0;
 #pragma unroll
-      for (int c = 0; c < 8; ++c) dma16<true>(kb, koff[c], lds_offset(slot + c * 1024));
+      for (int c = 0; c < 8; ++c) {
+        // paged: the page base was read from the block table by v_readlane
+        if constexpr (PAGED)
+          dma16<true>(kb, koff[c], lds_offset(slot + c * 1024));
+        else
+          dma16_sbase<true>(kb, koff[c], lds_offset(slot + c * 1024));
+      }
 #pragma unroll
-      for (int c = 0; c < 8; ++c) dma16<true>(vb, voff[c], lds_offset(slot + RTILE + c * 1024));
+      for (int c = 0; c < 8; ++c) {
+        if constexpr (PAGED)
+          dma16<true>(vb, voff[c], lds_offset(slot + RTILE + c * 1024));
+        else
+          dma16_sbase<true>(vb, voff[c], lds_offset(slot + RTILE + c * 1024));
+      }
     } else {  // tail: rows past the sequence re-read its last token (masked)
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
@@ -375,9 +386,9 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
     if (tb + RSTEP <= a.L) {
       const char *kb = kbase + (int64_t)tb * DH, *vb = vbase + (int64_t)tb * DH;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) dma16<true>(kb, off[c], lds_offset(slot + c * 1024));
+      for (int c = 0; c < 4; ++c) dma16_sbase<true>(kb, off[c], lds_offset(slot + c * 1024));
 #pragma unroll
-      for (int c = 0; c < 4; ++c) dma16<true>(vb, off[c], lds_offset(slot + R8TILE + c * 1024));
+      for (int c = 0; c < 4; ++c) dma16_sbase<true>(vb, off[c], lds_offset(slot + R8TILE + c * 1024));
     } else {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {

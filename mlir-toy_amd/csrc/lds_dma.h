@@ -63,6 +63,25 @@ __device__ inline void dma16(const char *sbase, uint32_t voff, uint32_t lds_addr
                  : "v"(voff), "s"(uniform_ptr(sbase)), "0"(__builtin_amdgcn_readfirstlane(lds_addr))
                  : "memory");
 }
+// The same copy when the base comes from scalar instructions only (kernel
+// arguments, work-group ids and uniform loop counters): no VALU writes those
+// SGPRs, so only the M0 wait state is needed. Which form a copy needs is a
+// property of the compiled code, not of the source: the ISA test in
+// tests/test_isa_hazards.py checks every copy of the built kernels.
+template <bool NT = false>
+__device__ inline void dma16_sbase(const char *sbase, uint32_t voff, uint32_t lds_addr) {
+  uint32_t m0;
+  if (NT)
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
+                 : "={m0}"(m0)
+                 : "v"(voff), "s"(uniform_ptr(sbase)), "0"(__builtin_amdgcn_readfirstlane(lds_addr))
+                 : "memory");
+  else
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 : "={m0}"(m0)
+                 : "v"(voff), "s"(uniform_ptr(sbase)), "0"(__builtin_amdgcn_readfirstlane(lds_addr))
+                 : "memory");
+}
 template <bool NT = false>
 __device__ inline void dma16(const char *addr, uint32_t lds_addr) {
   uint32_t m0;
