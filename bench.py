@@ -5,8 +5,8 @@ Default workload (the configuration BASELINE.json's metric is quoted on,
 configs[1]): causal bf16 prefill flash-attention B=4 H=32 S=4096 D=128 with
 per-row logsumexp, inputs ~ 0.5 N(0,1) resident in HBM. A step is one
 neptune_attn_fwd launch over that batch. The JSON line also carries, under
-"secondary", the split-K GQA decode (bf16 and fp8 KV) and selective-scan
-configurations measured the same way (GB/s against HBM).
+"secondary", the split-K GQA decode (bf16 and fp8 KV, contiguous and paged)
+and selective-scan configurations measured the same way (GB/s against HBM).
 
 Each workload first runs untimed for SPINUP_S seconds (so the GPU is at its
 working clocks), then W warmup steps, then exactly K timed steps.
@@ -126,18 +126,31 @@ def bench_decode(ops, torch, steps, warmup, fp8):
     return name, wall, ev, nbytes
 
 
-def bench_decode_paged(ops, torch, steps, warmup, page_size=64):
-    """Config 3 with K/V held in a shuffled page pool, token-major pages
-    [pages, page_size, Hkv, D] (seen as [pages, Hkv, page_size, D]) and a
-    random block table: same bytes as contiguous decode, scattered in HBM."""
+def bench_decode_paged(ops, torch, steps, warmup, page_size=64, fp8=False):
+    """Config 3 (fp8: config 5) with K/V held in a shuffled page pool and a
+    random block table: same bytes as contiguous decode, scattered in HBM.
+    bf16 pages are token-major [pages, page_size, Hkv, D] (seen as
+    [pages, Hkv, page_size, D]). fp8 pages are head-major
+    [pages, Hkv, page_size, D], hold finite positive E4M3 codes and one scale
+    per (page, kv head): a token-major fp8 page leaves each kv head only a
+    128-byte run per token, which HBM serves at about 0.61 of peak against
+    0.73 for head-major pages."""
     B, Hq, Hk, L, D, splits = 16, 32, 8, 32768, 128, 16
     per = L // page_size
     npages = B * per
     g = torch.Generator(device="cuda").manual_seed(4)
     q = torch.randn((B, Hq, D), device="cuda", generator=g).to(torch.bfloat16)
-    k_pool = torch.randn((npages, page_size, Hk, D), device="cuda", generator=g).to(torch.bfloat16)
-    v_pool = torch.randn((npages, page_size, Hk, D), device="cuda", generator=g).to(torch.bfloat16)
-    kp, vp = k_pool.permute(0, 2, 1, 3), v_pool.permute(0, 2, 1, 3)
+    pshape = (npages, Hk, page_size, D) if fp8 else (npages, page_size, Hk, D)
+    if fp8:
+        k_pool = torch.randint(0, 0x7f, pshape, device="cuda", generator=g, dtype=torch.uint8)
+        v_pool = torch.randint(0, 0x7f, pshape, device="cuda", generator=g, dtype=torch.uint8)
+        scales = {n: torch.rand((npages, Hk), device="cuda", generator=g) / 448 + 1e-3
+                  for n in ("k_scales", "v_scales")}
+    else:
+        k_pool = torch.randn(pshape, device="cuda", generator=g).to(torch.bfloat16)
+        v_pool = torch.randn(pshape, device="cuda", generator=g).to(torch.bfloat16)
+        scales = {}
+    kp, vp = (k_pool, v_pool) if fp8 else (k_pool.permute(0, 2, 1, 3), v_pool.permute(0, 2, 1, 3))
     table = torch.randperm(npages, device="cuda", generator=g).to(torch.int32).view(B, per)
     lens = torch.full((B,), L, dtype=torch.int32, device="cuda")
     k_meta = torch.empty((B, Hk, L, D), dtype=torch.bfloat16, device="meta")
@@ -146,10 +159,16 @@ def bench_decode_paged(ops, torch, steps, warmup, page_size=64):
     torch.cuda.synchronize()
 
     def step(_):
-        ops.decode_paged(q, kp, vp, table, lens, max_seq_len=L, num_splits=splits, workspace=ws)
+        ops.decode_paged(q, kp, vp, table, lens, max_seq_len=L, num_splits=splits, workspace=ws,
+                         **scales)
 
     wall, ev = time_launches(step, steps, warmup)
-    nbytes = 2 * B * Hk * L * D * 2 + B * per * 4 + 2 * B * Hq * D * 2
+    esize = 1 if fp8 else 2
+    nbytes = 2 * B * Hk * L * D * esize + B * per * 4 + 2 * B * Hq * D * 2
+    if fp8:
+        nbytes += 2 * B * per * Hk * 4  # the scales of every page read
+        return ("config5 fp8-KV split-K GQA decode, paged KV (64-token head-major pages)", wall,
+                ev, nbytes)
     return "config3 bf16 split-K GQA decode, paged KV (64-token pages)", wall, ev, nbytes
 
 
@@ -256,8 +275,8 @@ def main():
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the decode/scan configurations")
     ap.add_argument("--workload", default="all",
-                    choices=["all", "prefill", "decode", "decode_fp8", "decode_paged", "scan",
-                             "copy"],
+                    choices=["all", "prefill", "decode", "decode_fp8", "decode_paged",
+                             "decode_paged_fp8", "scan", "copy"],
                     help="run one configuration only (for profiling); 'copy' is a plain "
                          "1 GiB device copy used to calibrate HBM byte counters")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
@@ -287,6 +306,8 @@ def main():
         "decode": lambda: bench_decode(ops, torch, args.steps, args.warmup, fp8=False),
         "decode_fp8": lambda: bench_decode(ops, torch, args.steps, args.warmup, fp8=True),
         "decode_paged": lambda: bench_decode_paged(ops, torch, args.steps, args.warmup),
+        "decode_paged_fp8": lambda: bench_decode_paged(ops, torch, args.steps, args.warmup,
+                                                       fp8=True),
         "scan": lambda: bench_scan(ops, torch, args.steps, args.warmup),
         "copy": lambda: bench_copy(torch, args.steps, args.warmup),
     }
@@ -312,6 +333,8 @@ def main():
                                                             True)),
                         ("decode_paged", lambda: bench_decode_paged(ops, torch, sec_steps,
                                                                     sec_warm)),
+                        ("decode_paged_fp8", lambda: bench_decode_paged(ops, torch, sec_steps,
+                                                                        sec_warm, fp8=True)),
                         ("scan", lambda: bench_scan(ops, torch, sec_steps, sec_warm))):
             name, wall, ev, nbytes = fn()
             secondary.append(hbm_entry(key, name, wall, ev, nbytes, sec_steps, traffic))

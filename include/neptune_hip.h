@@ -200,6 +200,25 @@ NEPTUNE_API neptune_status neptune_decode_paged(const neptune_decode_desc *desc,
                                     void *workspace, size_t workspace_bytes,
                                     void *stream);
 
+/* Split-K decode over paged pools of E4M3FN codes. No counterpart in the
+ * reference: neptune_decode_paged with the fp8 KV of neptune_decode_splitk.
+ * desc->kv_dtype must be FP8_E4M3. Each page holds one fp32 scale per kv
+ * head for K and for V: k_scales, v_scales [num_pages, heads_kv]
+ * contiguous (desc->scale_block must be 0 or page_size); the dequantised
+ * value of a code in page p, kv head h is code * scale[p * heads_kv + h].
+ * Pool strides are in elements (bytes) and must be multiples of 16; the
+ * rest is as in neptune_decode_paged. */
+NEPTUNE_API neptune_status neptune_decode_paged_fp8(const neptune_decode_desc *desc,
+                                        const neptune_paged_kv_desc *pages,
+                                        const void *q, const uint8_t *k_pages,
+                                        const uint8_t *v_pages,
+                                        const float *k_scales,
+                                        const float *v_scales,
+                                        const int32_t *block_table,
+                                        const int32_t *seq_lens, void *o,
+                                        float *lse, void *workspace,
+                                        size_t workspace_bytes, void *stream);
+
 /* ---- selective scan ---------------------------------------------------- */
 
 NEPTUNE_API neptune_status neptune_selective_scan_fwd(

@@ -277,33 +277,76 @@ neptune_status neptune_decode_splitk(const neptune_decode_desc *d, const void *q
                     workspace_bytes, stream);
 }
 
+namespace {
+// checks shared by the two paged entry points; esize: bytes per pool element
+neptune_status paged_check(const char *fn, const neptune_decode_desc *d,
+                           const neptune_paged_kv_desc *pk, const void *q, const void *k_pages,
+                           const void *v_pages, const int32_t *block_table,
+                           const int32_t *seq_lens, const void *o, int64_t esize) {
+  neptune_status st = decode_check(d);
+  if (st != NEPTUNE_OK) return st;
+  if (!pk) return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "%s: pages desc is NULL", fn);
+  if (!q || !k_pages || !v_pages || !block_table || !seq_lens || !o)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT,
+                "%s: q, pools, block_table, seq_lens and o must be non-NULL", fn);
+  if (pk->num_pages <= 0 || pk->page_size <= 0 || pk->max_pages <= 0)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT,
+                "%s: num_pages, page_size and max_pages must be positive", fn);
+  if (pk->max_pages * pk->page_size < d->seq_kv)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT,
+                "%s: max_pages (%lld) * page_size (%lld) < seq_kv (%lld)", fn,
+                (long long)pk->max_pages, (long long)pk->page_size, (long long)d->seq_kv);
+  // 16-byte copy units: strides in whole units
+  const int64_t unit = 16 / esize;
+  for (int i = 0; i < 3; ++i)
+    if (pk->k_stride[i] <= 0 || pk->v_stride[i] <= 0 || pk->k_stride[i] % unit ||
+        pk->v_stride[i] % unit)
+      return fail(NEPTUNE_ERR_UNSUPPORTED,
+                  "%s: pool strides must be positive multiples of %lld elements", fn,
+                  (long long)unit);
+  return NEPTUNE_OK;
+}
+}  // namespace
+
 neptune_status neptune_decode_paged(const neptune_decode_desc *d, const neptune_paged_kv_desc *pk,
                                     const void *q, const void *k_pages, const void *v_pages,
                                     const int32_t *block_table, const int32_t *seq_lens, void *o,
                                     float *lse, void *workspace, size_t workspace_bytes,
                                     void *stream) {
-  neptune_status st = decode_check(d);
+  neptune_status st =
+      paged_check("decode_paged", d, pk, q, k_pages, v_pages, block_table, seq_lens, o, 2);
   if (st != NEPTUNE_OK) return st;
-  if (!pk) return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode_paged: pages desc is NULL");
-  if (!q || !k_pages || !v_pages || !block_table || !seq_lens || !o)
-    return fail(NEPTUNE_ERR_INVALID_ARGUMENT,
-                "decode_paged: q, pools, block_table, seq_lens and o must be non-NULL");
   if (d->kv_dtype != NEPTUNE_DTYPE_BF16)
-    return fail(NEPTUNE_ERR_UNSUPPORTED, "decode_paged: kv_dtype must be BF16");
-  if (pk->num_pages <= 0 || pk->page_size <= 0 || pk->max_pages <= 0)
-    return fail(NEPTUNE_ERR_INVALID_ARGUMENT,
-                "decode_paged: num_pages, page_size and max_pages must be positive");
-  if (pk->max_pages * pk->page_size < d->seq_kv)
-    return fail(NEPTUNE_ERR_INVALID_ARGUMENT,
-                "decode_paged: max_pages (%lld) * page_size (%lld) < seq_kv (%lld)",
-                (long long)pk->max_pages, (long long)pk->page_size, (long long)d->seq_kv);
-  for (int i = 0; i < 3; ++i)
-    if (pk->k_stride[i] <= 0 || pk->v_stride[i] <= 0 || pk->k_stride[i] % 8 ||
-        pk->v_stride[i] % 8)
-      return fail(NEPTUNE_ERR_UNSUPPORTED,
-                  "decode_paged: pool strides must be positive multiples of 8 elements");
+    return fail(NEPTUNE_ERR_UNSUPPORTED,
+                "decode_paged: kv_dtype must be BF16 (fp8 pools: neptune_decode_paged_fp8)");
   return decode_run(d, pk, q, k_pages, v_pages, nullptr, nullptr, block_table, seq_lens, o, lse,
                     workspace, workspace_bytes, stream);
+}
+
+neptune_status neptune_decode_paged_fp8(const neptune_decode_desc *d,
+                                        const neptune_paged_kv_desc *pk, const void *q,
+                                        const uint8_t *k_pages, const uint8_t *v_pages,
+                                        const float *k_scales, const float *v_scales,
+                                        const int32_t *block_table, const int32_t *seq_lens,
+                                        void *o, float *lse, void *workspace,
+                                        size_t workspace_bytes, void *stream) {
+  neptune_status st =
+      paged_check("decode_paged_fp8", d, pk, q, k_pages, v_pages, block_table, seq_lens, o, 1);
+  if (st != NEPTUNE_OK) return st;
+  if (d->kv_dtype != NEPTUNE_DTYPE_FP8_E4M3)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode_paged_fp8: kv_dtype must be FP8_E4M3");
+  if (!k_scales || !v_scales)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT,
+                "decode_paged_fp8: k_scales and v_scales must be non-NULL");
+  if (d->scale_block != 0 && d->scale_block != pk->page_size)
+    return fail(NEPTUNE_ERR_UNSUPPORTED,
+                "decode_paged_fp8: one scale per page: scale_block must be 0 or page_size "
+                "(%lld), not %lld",
+                (long long)pk->page_size, (long long)d->scale_block);
+  neptune_decode_desc dd = *d;
+  dd.scale_block = pk->page_size;
+  return decode_run(&dd, pk, q, k_pages, v_pages, k_scales, v_scales, block_table, seq_lens, o,
+                    lse, workspace, workspace_bytes, stream);
 }
 
 neptune_status neptune_kv_quantize_fp8(int64_t batch, int64_t heads_kv, int64_t seq_kv,

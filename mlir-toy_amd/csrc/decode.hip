@@ -351,6 +351,7 @@ constexpr int R8LDS = R8W * R8WAVE;
 typedef int v2i32 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) v2i32 lds_v2i32;
 
+template <bool PAGED>
 __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -361,42 +362,88 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
   const int bk = id / a.splits;
   const int b = bk / a.Hk, hk = bk % a.Hk;
   const int Gq = a.group;
+  // this sequence's length (paged: its own; out-of-range values clamped)
+  const int Lb = PAGED ? min(max(a.seqlens[b], 0), a.L) : a.L;
 
   const int c0 = split * a.chunk;
-  const int c1 = min(c0 + a.chunk, a.L);
+  const int c1 = min(c0 + a.chunk, Lb);
   const int wlen = ((a.chunk + R8W * RSTEP - 1) / (R8W * RSTEP)) * RSTEP;
   const int t0 = c0 + w * wlen;
   const int t1 = min(t0 + wlen, c1);
   const int nsteps = t1 > t0 ? (t1 - t0 + RSTEP - 1) / RSTEP : 0;
 
   const uint8_t *ring = smem + w * R8WAVE;
-  const char *kbase = (const char *)a.k + (int64_t)bk * a.L * DH;
-  const char *vbase = (const char *)a.v + (int64_t)bk * a.L * DH;
+  // token-row stride in bytes (a code is one byte); contiguous KV: row t of
+  // (b, kv head) at (bk * L + t) * DH
+  const int64_t tokb = PAGED ? (int64_t)a.tok : DH;
+  const char *kbase =
+      (const char *)a.k + (PAGED ? (int64_t)hk * a.k_ps[1] : (int64_t)bk * a.L * DH);
+  const char *vbase =
+      (const char *)a.v + (PAGED ? (int64_t)hk * a.v_ps[1] : (int64_t)bk * a.L * DH);
+  // paged: 64 block-table entries held in a register for the copies (lane j
+  // holding entry tab0 + j), read with v_readlane, reloaded every 64 pages
+  int tab0 = 0, tabv = 0;
+  auto load_tab = [&](int first) {
+    tab0 = first;
+    const int j = first + lane;
+    tabv = j < a.maxp ? a.btab[(int64_t)b * a.maxp + j] : 0;
+  };
+  // bytes from kbase / vbase to the first row of the step at tb (a step
+  // never straddles a page; entries outside [0, npages) are clamped)
+  auto step_base = [&](int tb, int64_t *kb, int64_t *vb) {
+    if (PAGED) {
+      const int pi = tb / a.ps;
+      if (pi - tab0 >= 64) {
+        load_tab(pi);
+        settle(tabv);
+      }
+      int pg = __builtin_amdgcn_readlane(tabv, pi - tab0);
+      pg = min(max(pg, 0), a.npages - 1);
+      const int64_t in_page = (int64_t)(tb % a.ps) * tokb;
+      *kb = (int64_t)pg * a.k_ps[0] + in_page;
+      *vb = (int64_t)pg * a.v_ps[0] + in_page;
+    } else {
+      *kb = *vb = (int64_t)tb * DH;
+    }
+  };
   // DMA chunk c covers rows 8c .. 8c+7; this lane moves row 8c + lane/8,
   // physical unit lane & 7
   uint32_t off[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int r = 8 * c + (lane >> 3);
-    off[c] = (uint32_t)(r * DH + (((lane & 7) ^ ((r >> 1) & 7)) << 4));
+    off[c] = (uint32_t)(r * tokb + (((lane & 7) ^ ((r >> 1) & 7)) << 4));
   }
   auto issue = [&](int i) {
     const int tb = t0 + i * RSTEP;
     const uint8_t *slot = ring + (i % R8NS) * R8SLOT;
-    if (tb + RSTEP <= a.L) {
-      const char *kb = kbase + (int64_t)tb * DH, *vb = vbase + (int64_t)tb * DH;
+    int64_t kb0, vb0;
+    step_base(tb, &kb0, &vb0);
+    if (tb + RSTEP <= Lb) {
+      const char *kb = kbase + kb0, *vb = vbase + vb0;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) dma16_sbase<true>(kb, off[c], lds_offset(slot + c * 1024));
+      for (int c = 0; c < 4; ++c) {
+        // paged: the page base was read from the block table by v_readlane
+        if constexpr (PAGED)
+          dma16<true>(kb, off[c], lds_offset(slot + c * 1024));
+        else
+          dma16_sbase<true>(kb, off[c], lds_offset(slot + c * 1024));
+      }
 #pragma unroll
-      for (int c = 0; c < 4; ++c) dma16_sbase<true>(vb, off[c], lds_offset(slot + R8TILE + c * 1024));
-    } else {
+      for (int c = 0; c < 4; ++c) {
+        if constexpr (PAGED)
+          dma16<true>(vb, off[c], lds_offset(slot + R8TILE + c * 1024));
+        else
+          dma16_sbase<true>(vb, off[c], lds_offset(slot + R8TILE + c * 1024));
+      }
+    } else {  // tail: rows past the sequence re-read its last token (masked)
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int r = 8 * c + (lane >> 3);
-        const int64_t row = min(tb + r, a.L - 1);
+        const int64_t row = min(tb + r, Lb - 1) - tb;
         const int u = ((lane & 7) ^ ((r >> 1) & 7)) << 4;
-        dma16<true>(kbase + row * DH + u, lds_offset(slot + c * 1024));
-        dma16<true>(vbase + row * DH + u, lds_offset(slot + R8TILE + c * 1024));
+        dma16<true>(kbase + kb0 + row * tokb + u, lds_offset(slot + c * 1024));
+        dma16<true>(vbase + vb0 + row * tokb + u, lds_offset(slot + R8TILE + c * 1024));
       }
     }
   };
@@ -412,24 +459,37 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
   }
   // the K / V scales of 64 scale blocks of this wave's range in registers,
   // lane j holding block blk0 + j: a step takes its scales with v_readlane
-  // instead of a memory load; reloaded every 64 blocks
+  // instead of a memory load; reloaded every 64 blocks. Paged, a block is a
+  // page (one scale per page and kv head) and lane j holds the scales of
+  // block-table entry blk0 + j: this window is separate from the copies'
+  // one, which runs up to two steps ahead of the math
+  const int bsz = PAGED ? a.ps : a.sb;  // tokens per scale block
   int blk0 = 0;
   float kscv = 0.0f, vscv = 0.0f;
   auto load_scales = [&](int first) {
     blk0 = first;
     const int j = first + lane;
-    kscv = j < a.nsb ? a.ksc[(int64_t)bk * a.nsb + j] : 0.0f;
-    vscv = j < a.nsb ? a.vsc[(int64_t)bk * a.nsb + j] : 0.0f;
+    if (PAGED) {
+      int pg = j < a.maxp ? a.btab[(int64_t)b * a.maxp + j] : 0;
+      pg = min(max(pg, 0), a.npages - 1);
+      kscv = a.ksc[(int64_t)pg * a.Hk + hk];
+      vscv = a.vsc[(int64_t)pg * a.Hk + hk];
+    } else {
+      kscv = j < a.nsb ? a.ksc[(int64_t)bk * a.nsb + j] : 0.0f;
+      vscv = j < a.nsb ? a.vsc[(int64_t)bk * a.nsb + j] : 0.0f;
+    }
   };
-  load_scales(t0 / a.sb);
+  load_scales(t0 / bsz);
+  if (PAGED) load_tab(t0 / a.ps);
   // scale block of the current step, kept by counting (a step is 32 tokens
   // and a block a multiple of 32, so steps never straddle blocks)
-  int blk = t0 / a.sb, in_blk = t0 - blk * a.sb;
-  // Q and the scales land before the first copy is issued
+  int blk = t0 / bsz, in_blk = t0 - blk * bsz;
+  // Q, the scales and the table land before the first copy is issued
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) settle(qf[ks]);
   settle(kscv);
   settle(vscv);
+  if (PAGED) settle(tabv);
 #pragma unroll
   for (int i = 0; i < R8NS; ++i)
     if (i < nsteps) issue(i);
@@ -541,7 +601,7 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
     if (i + R8NS < nsteps) issue(i + R8NS);
     in_blk += RSTEP;
-    if (in_blk == a.sb) {
+    if (in_blk == bsz) {
       in_blk = 0;
       ++blk;
     }
@@ -731,15 +791,16 @@ bool decode_supported(const DecodeLaunch &a, const char **why) {
     return false;
   }
   if (a.block_table) {
-    if (a.kv_dtype == 3) {
-      *why = "paged decode supports bf16 KV";
-      return false;
-    }
     if (a.page_size % STEP) {
       *why = "paged decode needs a page size that is a multiple of 32 tokens";
       return false;
     }
-    if (a.k_pstride[2] != a.v_pstride[2] || 31 * a.k_pstride[2] * 2 + 256 > ((int64_t)1 << 31) ||
+    if (a.kv_dtype == 3 && a.scale_block != a.page_size) {
+      *why = "paged fp8 decode takes one scale per page (scale_block 0 or page_size)";
+      return false;
+    }
+    const int64_t esize = a.kv_dtype == 3 ? 1 : 2;
+    if (a.k_pstride[2] != a.v_pstride[2] || 31 * a.k_pstride[2] * esize + 256 > ((int64_t)1 << 31) ||
         a.num_pages > ((int64_t)1 << 31) - 1 || a.max_pages > ((int64_t)1 << 31) - 1) {
       *why = "paged decode needs equal K/V token strides below 64 MiB and fewer than 2^31 pages";
       return false;
@@ -787,10 +848,18 @@ hipError_t launch_decode(const DecodeLaunch &L, hipStream_t s) {
   // statics are initialised exactly once, also under concurrent first calls);
   // a failure is kept and returned by every later launch.
   if (L.kv_dtype == 3) {
-    static const hipError_t attr8 = hipFuncSetAttribute(
-        (const void *)decode_partial_ring8, hipFuncAttributeMaxDynamicSharedMemorySize, R8LDS);
+    static const hipError_t attr8_c = hipFuncSetAttribute(
+        (const void *)decode_partial_ring8<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        R8LDS);
+    static const hipError_t attr8_p = hipFuncSetAttribute(
+        (const void *)decode_partial_ring8<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        R8LDS);
+    const hipError_t attr8 = paged ? attr8_p : attr8_c;
     if (attr8 != hipSuccess) return attr8;
-    hipLaunchKernelGGL(decode_partial_ring8, dim3(grid), dim3(R8T), R8LDS, s, a);
+    if (paged)
+      hipLaunchKernelGGL(decode_partial_ring8<true>, dim3(grid), dim3(R8T), R8LDS, s, a);
+    else
+      hipLaunchKernelGGL(decode_partial_ring8<false>, dim3(grid), dim3(R8T), R8LDS, s, a);
   } else {
     static const hipError_t attr_c = hipFuncSetAttribute(
         (const void *)decode_partial_ring<false>, hipFuncAttributeMaxDynamicSharedMemorySize, RLDS);

@@ -43,6 +43,7 @@ EXPORTED_SYMBOLS = (
     "neptune_decode_workspace_bytes",
     "neptune_decode_splitk",
     "neptune_decode_paged",
+    "neptune_decode_paged_fp8",
     "neptune_kv_quantize_fp8",
     "neptune_selective_scan_fwd",
 )
@@ -217,6 +218,11 @@ def _declare(lib: ctypes.CDLL) -> None:
         ctypes.c_size_t, vp,
     ]
     lib.neptune_decode_paged.restype = i32
+    lib.neptune_decode_paged_fp8.argtypes = [
+        ctypes.POINTER(DecodeDesc), ctypes.POINTER(PagedKvDesc), vp, vp, vp, vp, vp, vp, vp, vp,
+        vp, vp, ctypes.c_size_t, vp,
+    ]
+    lib.neptune_decode_paged_fp8.restype = i32
     lib.neptune_kv_quantize_fp8.argtypes = [i64, i64, i64, i64, i64, vp, vp, vp, vp]
     lib.neptune_kv_quantize_fp8.restype = i32
     lib.neptune_selective_scan_fwd.argtypes = [

@@ -235,21 +235,26 @@ def decode_paged(
     scale: float | None = None,
     return_lse: bool = False,
     workspace: torch.Tensor | None = None,
+    k_scales: torch.Tensor | None = None,
+    v_scales: torch.Tensor | None = None,
 ):
     """Split-K decode over a paged KV cache.
 
-    q [B, Hq, D] bf16; k_pages / v_pages bf16 [num_pages, Hkv, page_size, D]
+    q [B, Hq, D] bf16; k_pages / v_pages [num_pages, Hkv, page_size, D]
     views (any page/head/position strides with D contiguous, e.g. a permuted
-    [num_pages, page_size, Hkv, D] pool); block_table [B, max_pages] and
+    [num_pages, page_size, Hkv, D] pool) of bf16, or of E4M3 codes (uint8 /
+    torch.float8_e4m3fn) with k_scales / v_scales fp32 [num_pages, Hkv]
+    (one scale per page and kv head); block_table [B, max_pages] and
     seq_lens [B] int32 on the device. ``max_seq_len`` (default
     max_pages * page_size) is the longest sequence and sets the split
     layout. Returns o [B, Hq, D] bf16.
     """
     q3 = _as_q3(q)
-    _require_cuda(q3, k_pages, v_pages, block_table, seq_lens, workspace)
-    if q3.dtype != torch.bfloat16 or k_pages.dtype != torch.bfloat16 or \
-            v_pages.dtype != torch.bfloat16:
-        raise ValueError("paged decode takes bfloat16 q and KV pages")
+    _require_cuda(q3, k_pages, v_pages, block_table, seq_lens, workspace, k_scales, v_scales)
+    fp8 = k_pages.dtype in (torch.uint8, torch.float8_e4m3fn)
+    if q3.dtype != torch.bfloat16 or k_pages.dtype != v_pages.dtype or \
+            not (fp8 or k_pages.dtype == torch.bfloat16):
+        raise ValueError("paged decode takes bfloat16 q and bfloat16 or E4M3 KV pages")
     if k_pages.dim() != 4 or tuple(k_pages.shape) != tuple(v_pages.shape) or \
             k_pages.stride(-1) != 1 or v_pages.stride(-1) != 1:
         raise ValueError("k_pages / v_pages: matching [pages, Hkv, page_size, D] views, D contiguous")
@@ -257,13 +262,19 @@ def decode_paged(
         if t.dtype != torch.int32 or not t.is_contiguous():
             raise ValueError(f"{name} must be a contiguous int32 tensor")
     npages, Hk, psize, D = k_pages.shape
+    if fp8:
+        for name, t in (("k_scales", k_scales), ("v_scales", v_scales)):
+            if t is None or t.dtype != torch.float32 or not t.is_contiguous() or \
+                    tuple(t.shape) != (npages, Hk):
+                raise ValueError(f"fp8 pages need {name}: contiguous float32 [num_pages, Hkv]")
     B = q3.shape[0]
     if block_table.dim() != 2 or block_table.shape[0] != B or tuple(seq_lens.shape) != (B,):
         raise ValueError("block_table [B, max_pages] and seq_lens [B] must match q's batch")
     max_pages = block_table.shape[1]
     L = int(max_seq_len) if max_seq_len is not None else max_pages * psize
     k4 = torch.empty((B, Hk, L, D), dtype=k_pages.dtype, device="meta")
-    desc = _decode_desc(q3, k4, num_splits, 64, scale, _abi.DTYPE_BF16)
+    desc = _decode_desc(q3, k4, num_splits, psize if fp8 else 64, scale,
+                        _abi.DTYPE_FP8_E4M3 if fp8 else _abi.DTYPE_BF16)
     pk = _abi.PagedKvDesc()
     pk.num_pages, pk.page_size, pk.max_pages = npages, psize, max_pages
     pk.k_stride[:] = (k_pages.stride(0), k_pages.stride(1), k_pages.stride(2))
@@ -275,16 +286,19 @@ def decode_paged(
         workspace = torch.empty(max(n.value, 1), dtype=torch.uint8, device=q3.device)
     out = torch.empty_like(q3)
     lse = torch.empty(q3.shape[:2], dtype=torch.float32, device=q3.device) if return_lse else None
+    tail = (block_table.data_ptr(), seq_lens.data_ptr(), out.data_ptr(),
+            lse.data_ptr() if lse is not None else None, workspace.data_ptr(),
+            workspace.numel() * workspace.element_size(), _stream(q3))
     with torch.cuda.device(q3.device):
-        check(
-            lib.neptune_decode_paged(
+        if fp8:
+            st = lib.neptune_decode_paged_fp8(
                 ctypes.byref(desc), ctypes.byref(pk), q3.data_ptr(), k_pages.data_ptr(),
-                v_pages.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(), out.data_ptr(),
-                lse.data_ptr() if lse is not None else None, workspace.data_ptr(),
-                workspace.numel() * workspace.element_size(), _stream(q3),
-            ),
-            lib,
-        )
+                v_pages.data_ptr(), k_scales.data_ptr(), v_scales.data_ptr(), *tail)
+        else:
+            st = lib.neptune_decode_paged(
+                ctypes.byref(desc), ctypes.byref(pk), q3.data_ptr(), k_pages.data_ptr(),
+                v_pages.data_ptr(), *tail)
+        check(st, lib)
     return (out, lse) if return_lse else out
 
 

@@ -131,6 +131,11 @@ def lib() -> ctypes.CDLL:
             ctypes.POINTER(DecodeDesc), ctypes.POINTER(PagedKvDesc), vp, vp, vp, vp, vp, vp, vp,
         ]
         L.neptune_cpu_decode_paged.restype = i32
+        L.neptune_cpu_decode_paged_fp8.argtypes = [
+            ctypes.POINTER(DecodeDesc), ctypes.POINTER(PagedKvDesc), vp, vp, vp, vp, vp, vp, vp,
+            vp, vp,
+        ]
+        L.neptune_cpu_decode_paged_fp8.restype = i32
         L.neptune_cpu_decode_layout.argtypes = [
             ctypes.POINTER(DecodeDesc), ctypes.POINTER(i64), ctypes.POINTER(i64),
         ]
@@ -260,33 +265,51 @@ def decode_splitk(q, k, v, kv_dtype: int = BF16, k_scale=None, v_scale=None,
 
 
 def decode_paged(q, k_pool, v_pool, block_table, seq_lens, max_seq_len=None,
-                 num_splits: int = 0, scale_log2: float = 0.0):
+                 num_splits: int = 0, scale_log2: float = 0.0, k_scales=None, v_scales=None):
     """Split-K decode over a paged pool. q [B,Hq,D] bf16 bits; k_pool /
-    v_pool bf16 bits viewed as [pages, Hk, page_size, D] (any element strides
-    with D contiguous; read in place); block_table [B, max_pages] and
-    seq_lens [B] int32. Returns (o bits, lse)."""
+    v_pool viewed as [pages, Hk, page_size, D] (any element strides with D
+    contiguous; read in place): bf16 bits (uint16), or E4M3 codes (uint8)
+    with k_scales / v_scales float32 [pages, Hk], one scale per (page, kv
+    head); block_table [B, max_pages] and seq_lens [B] int32. Returns
+    (o bits, lse)."""
     q = np.ascontiguousarray(q)
     block_table = np.ascontiguousarray(block_table, dtype=np.int32)
     seq_lens = np.ascontiguousarray(seq_lens, dtype=np.int32)
+    fp8 = k_pool.dtype == np.uint8
+    esize = 1 if fp8 else 2
     for pool in (k_pool, v_pool):
-        if pool.dtype != np.uint16 or pool.ndim != 4 or pool.strides[3] != 2:
-            raise ValueError("pools must be uint16 [pages, Hk, page_size, D] with D contiguous")
+        if (pool.dtype != k_pool.dtype or pool.dtype not in (np.uint16, np.uint8)
+                or pool.ndim != 4 or pool.strides[3] != esize):
+            raise ValueError("pools must be uint16 (bf16) or uint8 (E4M3) "
+                             "[pages, Hk, page_size, D] with D contiguous")
     npages, Hk, ps, D = k_pool.shape
+    if fp8:
+        if k_scales is None or v_scales is None:
+            raise ValueError("fp8 pools need k_scales and v_scales [pages, Hk]")
+        k_scales = np.ascontiguousarray(k_scales, dtype=np.float32)
+        v_scales = np.ascontiguousarray(v_scales, dtype=np.float32)
+        if k_scales.shape != (npages, Hk) or v_scales.shape != (npages, Hk):
+            raise ValueError("k_scales / v_scales must be [pages, Hk]")
     L = int(max_seq_len) if max_seq_len is not None else block_table.shape[1] * ps
     d = DecodeDesc()
     d.batch, d.heads_q, d.heads_kv, d.seq_kv, d.head_dim = q.shape[0], q.shape[1], Hk, L, D
-    d.num_splits, d.scale_block = num_splits, 64
-    d.q_dtype, d.kv_dtype, d.scale_log2 = BF16, BF16, scale_log2
+    d.num_splits, d.scale_block = num_splits, (ps if fp8 else 64)
+    d.q_dtype, d.kv_dtype, d.scale_log2 = BF16, (FP8 if fp8 else BF16), scale_log2
     pk = PagedKvDesc()
     pk.num_pages, pk.page_size, pk.max_pages = npages, ps, block_table.shape[1]
-    pk.k_stride[:] = tuple(x // 2 for x in k_pool.strides[:3])
-    pk.v_stride[:] = tuple(x // 2 for x in v_pool.strides[:3])
+    pk.k_stride[:] = tuple(x // esize for x in k_pool.strides[:3])
+    pk.v_stride[:] = tuple(x // esize for x in v_pool.strides[:3])
     o = np.empty(q.shape, dtype=np.uint16)
     lse = np.empty(q.shape[:2], dtype=np.float32)
-    _check(lib().neptune_cpu_decode_paged(ctypes.byref(d), ctypes.byref(pk), _ptr(q),
-                                          k_pool.ctypes.data, v_pool.ctypes.data,
-                                          _ptr(block_table), _ptr(seq_lens), _ptr(o), _ptr(lse)),
-           "decode_paged")
+    if fp8:
+        st = lib().neptune_cpu_decode_paged_fp8(
+            ctypes.byref(d), ctypes.byref(pk), _ptr(q), k_pool.ctypes.data, v_pool.ctypes.data,
+            _ptr(k_scales), _ptr(v_scales), _ptr(block_table), _ptr(seq_lens), _ptr(o), _ptr(lse))
+    else:
+        st = lib().neptune_cpu_decode_paged(
+            ctypes.byref(d), ctypes.byref(pk), _ptr(q), k_pool.ctypes.data, v_pool.ctypes.data,
+            _ptr(block_table), _ptr(seq_lens), _ptr(o), _ptr(lse))
+    _check(st, "decode_paged")
     return o, lse
 
 

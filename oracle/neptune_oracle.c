@@ -255,14 +255,17 @@ typedef struct {
    * vpage) plus kbase / vbase, row t % page_size */
   const int32_t *btab;
   int64_t page_size, num_pages, kpage, vpage;
+  /* paged fp8: kscale / vscale hold one scale per page at this stride (the
+   * pool's [pages, heads_kv] rows, already offset to the KV head) */
+  int64_t scale_page_stride;
 } kv_view;
 
 static inline float kv_load(const kv_view *kv, int which, int64_t t,
                             int64_t dd) {
   const void *base = which ? kv->v : kv->k;
-  int64_t row = t, page_off = 0;
+  int64_t row = t, page_off = 0, pg = 0;
   if (kv->btab) {
-    int64_t pg = kv->btab[t / kv->page_size];
+    pg = kv->btab[t / kv->page_size];
     pg = pg < 0 ? 0 : (pg >= kv->num_pages ? kv->num_pages - 1 : pg);
     page_off = pg * (which ? kv->vpage : kv->kpage);
     row = t % kv->page_size;
@@ -271,7 +274,7 @@ static inline float kv_load(const kv_view *kv, int which, int64_t t,
                       : page_off + kv->kbase + row * kv->kstride + dd * kv->kdstride;
   float x = load_elem(base, off, kv->dt);
   const float *sc = which ? kv->vscale : kv->kscale;
-  if (sc) x *= sc[t / kv->scale_block];
+  if (sc) x *= kv->btab ? sc[pg * kv->scale_page_stride] : sc[t / kv->scale_block];
   return x;
 }
 
@@ -516,19 +519,25 @@ int32_t neptune_cpu_decode_splitk(const neptune_decode_desc *d, const void *q,
  * seq_kv, the longest sequence) and the same per-split recurrence and
  * combine as neptune_cpu_decode_splitk, with sequence b's tokens read
  * through its block-table row and only its first seq_lens[b] tokens (clamped
- * to [0, seq_kv]) visible. An empty sequence gives O = 0 and lse = -inf. */
-int32_t neptune_cpu_decode_paged(const neptune_decode_desc *d,
-                                 const neptune_paged_kv_desc *pk, const void *q,
-                                 const void *k_pages, const void *v_pages,
-                                 const int32_t *block_table,
-                                 const int32_t *seq_lens, void *o, float *lse) {
+ * to [0, seq_kv]) visible. An empty sequence gives O = 0 and lse = -inf.
+ * fp8 pools carry one scale per (page, kv head), k_scales / v_scales
+ * [num_pages, heads_kv], and then need scale_block 0 or page_size. */
+static int32_t decode_paged(const neptune_decode_desc *d, const neptune_paged_kv_desc *pk,
+                            const void *q, const void *k_pages, const void *v_pages,
+                            const float *k_scales, const float *v_scales,
+                            const int32_t *block_table, const int32_t *seq_lens, void *o,
+                            float *lse) {
   if (!d || !pk || !q || !k_pages || !v_pages || !block_table || !seq_lens || !o)
     return NEPTUNE_ERR_INVALID_ARGUMENT;
+  const int fp8 = d->kv_dtype == NEPTUNE_DTYPE_FP8_E4M3;
   if (d->heads_q <= 0 || d->heads_kv <= 0 || d->heads_q % d->heads_kv ||
-      d->head_dim <= 0 || d->kv_dtype != NEPTUNE_DTYPE_BF16)
+      d->head_dim <= 0 || (!fp8 && d->kv_dtype != NEPTUNE_DTYPE_BF16))
     return NEPTUNE_ERR_INVALID_ARGUMENT;
   if (pk->num_pages <= 0 || pk->page_size <= 0 || pk->max_pages <= 0 ||
       pk->max_pages * pk->page_size < d->seq_kv)
+    return NEPTUNE_ERR_INVALID_ARGUMENT;
+  if (fp8 && (!k_scales || !v_scales ||
+              (d->scale_block != 0 && d->scale_block != pk->page_size)))
     return NEPTUNE_ERR_INVALID_ARGUMENT;
   int64_t S, chunk;
   int st = neptune_cpu_decode_layout(d, &S, &chunk);
@@ -549,10 +558,11 @@ int32_t neptune_cpu_decode_paged(const neptune_decode_desc *d,
       kv_view kv = {.k = k_pages, .v = v_pages, .dt = d->kv_dtype,
                     .kbase = hk * pk->k_stride[1], .vbase = hk * pk->v_stride[1],
                     .kstride = pk->k_stride[2], .vstride = pk->v_stride[2], .kdstride = 1,
-                    .kscale = NULL, .vscale = NULL, .scale_block = 1, .p_dtype = d->q_dtype,
+                    .kscale = fp8 ? k_scales + hk : NULL, .vscale = fp8 ? v_scales + hk : NULL,
+                    .scale_block = 1, .p_dtype = d->q_dtype,
                     .btab = block_table + b * pk->max_pages, .page_size = pk->page_size,
                     .num_pages = pk->num_pages, .kpage = pk->k_stride[0],
-                    .vpage = pk->v_stride[0]};
+                    .vpage = pk->v_stride[0], .scale_page_stride = Hk};
       for (int64_t s = 0; s < S; ++s) {
         int64_t k0 = s * chunk, k1 = k0 + chunk < len ? k0 + chunk : len;
         htile_row(qrow, D, &kv, k0, k1, k1, scale2, ot + s * D, &ms[s], &ls[s]);
@@ -570,6 +580,26 @@ int32_t neptune_cpu_decode_paged(const neptune_decode_desc *d,
       free(buf);
     }
   return NEPTUNE_OK;
+}
+
+int32_t neptune_cpu_decode_paged(const neptune_decode_desc *d,
+                                 const neptune_paged_kv_desc *pk, const void *q,
+                                 const void *k_pages, const void *v_pages,
+                                 const int32_t *block_table,
+                                 const int32_t *seq_lens, void *o, float *lse) {
+  if (d && d->kv_dtype != NEPTUNE_DTYPE_BF16) return NEPTUNE_ERR_INVALID_ARGUMENT;
+  return decode_paged(d, pk, q, k_pages, v_pages, NULL, NULL, block_table, seq_lens, o, lse);
+}
+
+int32_t neptune_cpu_decode_paged_fp8(const neptune_decode_desc *d,
+                                     const neptune_paged_kv_desc *pk, const void *q,
+                                     const uint8_t *k_pages, const uint8_t *v_pages,
+                                     const float *k_scales, const float *v_scales,
+                                     const int32_t *block_table, const int32_t *seq_lens,
+                                     void *o, float *lse) {
+  if (d && d->kv_dtype != NEPTUNE_DTYPE_FP8_E4M3) return NEPTUNE_ERR_INVALID_ARGUMENT;
+  return decode_paged(d, pk, q, k_pages, v_pages, k_scales, v_scales, block_table, seq_lens,
+                      o, lse);
 }
 
 int32_t neptune_cpu_kv_quantize_fp8(int64_t batch, int64_t heads_kv,

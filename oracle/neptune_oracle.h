@@ -24,6 +24,10 @@
  *                   page layouts) at full lengths; ragged lengths against
  *                   attn_exact on each sequence's own tokens; empty sequence
  *                   and out-of-pool table entries
+ *   decode_paged_fp8 == decode_splitk (fp8, scale block = page size) bit for
+ *                   bit over a shuffled pool of the same codes and scales;
+ *                   ragged lengths against decode_splitk on each sequence's
+ *                   prefix
  *   kv_quantize     codes decode to within half an E4M3 ulp of x/scale,
  *                   scale = amax/448, block amax maps to code 0x7e
  *   selective_scan  brute-force numpy recurrence on tiny inputs; delta -> 0,
@@ -78,6 +82,15 @@ int32_t neptune_cpu_decode_paged(const neptune_decode_desc *d,
                                  const void *k_pages, const void *v_pages,
                                  const int32_t *block_table,
                                  const int32_t *seq_lens, void *o, float *lse);
+
+/* the same over fp8 E4M3 pools with one scale per (page, kv head)
+ * (neptune_decode_paged_fp8's twin) */
+int32_t neptune_cpu_decode_paged_fp8(const neptune_decode_desc *d,
+                                     const neptune_paged_kv_desc *pk, const void *q,
+                                     const uint8_t *k_pages, const uint8_t *v_pages,
+                                     const float *k_scales, const float *v_scales,
+                                     const int32_t *block_table, const int32_t *seq_lens,
+                                     void *o, float *lse);
 
 /* number of splits and tokens per split the decode path uses */
 int32_t neptune_cpu_decode_layout(const neptune_decode_desc *d,

@@ -315,6 +315,49 @@ def test_paged_decode_no_device_path(lib):
     assert _paged(lib, _dec_desc(), _pages()) == _abi.ERR_NO_DEVICE
 
 
+def _paged8(lib, d, p, ws_bytes=1 << 30, ptrs=(FAKE,) * 7):
+    """neptune_decode_paged_fp8 with q, k, v, k_scales, v_scales, block_table,
+    seq_lens = ptrs."""
+    return lib.neptune_decode_paged_fp8(ctypes.byref(d),
+                                        ctypes.byref(p) if p is not None else None,
+                                        *ptrs, FAKE, None, FAKE, ws_bytes, None)
+
+
+def _fp8_desc(**kw):
+    kw.setdefault("kv_dtype", _abi.DTYPE_FP8_E4M3)
+    kw.setdefault("scale_block", 0)
+    return _dec_desc(**kw)
+
+
+@pytest.mark.parametrize("dkw,pkw,status", [
+    ({"scale_block": 32}, {}, _abi.ERR_UNSUPPORTED),               # one scale per page only
+    ({"kv_dtype": _abi.DTYPE_BF16}, {}, _abi.ERR_INVALID_ARGUMENT),  # bf16 pools: decode_paged
+    ({}, {"k_stride": (2 * 64 * 128, 64 * 128, 136)}, _abi.ERR_UNSUPPORTED),  # not 16 bytes
+    ({}, {"page_size": 48}, _abi.ERR_UNSUPPORTED),
+    ({}, {"max_pages": 15}, _abi.ERR_INVALID_ARGUMENT),
+])
+def test_paged_fp8_decode_validation(lib, dkw, pkw, status):
+    assert _paged8(lib, _fp8_desc(**dkw), _pages(**pkw)) == status
+    assert lib.neptune_last_error()
+
+
+def test_paged_fp8_decode_null_arguments(lib):
+    assert _paged8(lib, _fp8_desc(), None) == _abi.ERR_INVALID_ARGUMENT
+    for i in range(7):
+        ptrs = [FAKE] * 7
+        ptrs[i] = None
+        assert _paged8(lib, _fp8_desc(), _pages(), ptrs=tuple(ptrs)) == _abi.ERR_INVALID_ARGUMENT
+    assert _paged8(lib, _fp8_desc(), _pages(), ws_bytes=16) == _abi.ERR_WORKSPACE_TOO_SMALL
+
+
+def test_paged_fp8_decode_no_device_path(lib):
+    if lib.neptune_device_count() > 0:
+        pytest.skip("a HIP device is visible; the no-device path is not reachable")
+    # scale_block 0 and scale_block == page_size are both accepted
+    assert _paged8(lib, _fp8_desc(), _pages()) == _abi.ERR_NO_DEVICE
+    assert _paged8(lib, _fp8_desc(scale_block=64), _pages()) == _abi.ERR_NO_DEVICE
+
+
 def test_quantize_and_scan_validation(lib):
     q = lib.neptune_kv_quantize_fp8
     assert q(1, 1, 64, 128, 64, None, FAKE, FAKE, None) == _abi.ERR_INVALID_ARGUMENT

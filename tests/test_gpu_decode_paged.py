@@ -8,6 +8,10 @@
   the whole batch against the oracle's paged twin (same split layout).
 * A zero-length sequence gives O = 0 and lse = -inf; block-table entries
   outside the pool are clamped by the kernel exactly as by the twin.
+* fp8 pools (neptune_decode_paged_fp8, one scale per page and kv head):
+  bit for bit equal to the contiguous fp8 decode whose scale block is the
+  page, for both pool layouts; ragged, empty and out-of-pool cases against
+  the oracle's fp8 paged twin.
 """
 
 import numpy as np
@@ -15,7 +19,7 @@ import pytest
 import torch
 
 import oracle
-from helpers import TOL_BF16_ABS, TOL_LSE_ABS, bits, randn, to_f32
+from helpers import TOL_BF16_ABS, TOL_FP8_ABS, TOL_LSE_ABS, bits, randn, to_f32
 
 pytestmark = pytest.mark.gpu
 
@@ -120,3 +124,74 @@ def test_paged_empty_sequence_and_bad_table(ops):
     to, _ = oracle.decode_paged(bits(q), bits(kp), bits(vp), bad.cpu().numpy(),
                                 lens.cpu().numpy(), max_seq_len=L)
     assert np.abs(to_f32(o2) - oracle.decode(to, oracle.BF16)).max() <= TOL_BF16_ABS
+
+
+def page_scales(scales, table, npages, seed):
+    """Per-(page, kv head) scales [npages, Hk] from per-block scales
+    [B, Hk, per]: block j of sequence b lives in page table[b, j]; pages no
+    sequence uses get unrelated scales, so a misread shows."""
+    B, Hk, per = scales.shape
+    g = torch.Generator().manual_seed(seed)
+    pool = (torch.rand((npages, Hk), generator=g) * 1.5 + 0.5).cuda()
+    for b in range(B):
+        pool[table[b].long()] = scales[b].t()
+    return pool.contiguous()
+
+
+def fp8_pools(ops, k, v, ps, seed, token_major=False):
+    kc, ks = ops.kv_quantize_fp8(k.cuda(), scale_block=ps)
+    vc, vs = ops.kv_quantize_fp8(v.cuda(), scale_block=ps)
+    kp, table = paginate(kc.cpu(), ps, seed=seed, token_major=token_major)
+    vp, _ = paginate(vc.cpu(), ps, seed=seed, token_major=token_major)
+    kps = page_scales(ks, table, kp.shape[0], seed + 1)
+    vps = page_scales(vs, table, kp.shape[0], seed + 2)
+    return (kc, ks, vc, vs), (kp, vp, kps, vps, table)
+
+
+@pytest.mark.parametrize("token_major", [False, True])
+def test_paged_fp8_equals_contiguous_bitwise(ops, token_major):
+    _log(f"case: paged fp8 == contiguous fp8, token_major={token_major}")
+    B, Hq, Hk, L, D, ps, splits = 2, 8, 2, 1024, 128, 64, 5
+    q = randn((B, Hq, D), seed=50).cuda()
+    k, v = randn((B, Hk, L, D), seed=51), randn((B, Hk, L, D), seed=52)
+    (kc, ks, vc, vs), (kp, vp, kps, vps, table) = fp8_pools(ops, k, v, ps, 53, token_major)
+    lens = torch.full((B,), L, dtype=torch.int32, device="cuda")
+    o_ref, lse_ref = ops.decode_splitk(q, kc, vc, k_scale=ks, v_scale=vs, num_splits=splits,
+                                       scale_block=ps, return_lse=True)
+    o, lse = ops.decode_paged(q, kp, vp, table, lens, max_seq_len=L, num_splits=splits,
+                              return_lse=True, k_scales=kps, v_scales=vps)
+    torch.cuda.synchronize()
+    assert torch.equal(o.view(torch.int16), o_ref.view(torch.int16))
+    assert torch.equal(lse, lse_ref)
+    to, tl = oracle.decode_paged(bits(q), kp.cpu().numpy(), vp.cpu().numpy(),
+                                 table.cpu().numpy(), lens.cpu().numpy(), max_seq_len=L,
+                                 num_splits=splits, k_scales=kps.cpu().numpy(),
+                                 v_scales=vps.cpu().numpy())
+    assert np.abs(to_f32(o) - oracle.decode(to, oracle.BF16)).max() <= TOL_FP8_ABS
+    assert np.abs(to_f32(lse) - tl).max() <= TOL_LSE_ABS
+
+
+@pytest.mark.parametrize("ps", [32, 128, 256])
+def test_paged_fp8_ragged_empty_and_bad_table(ops, ps):
+    _log(f"case: paged fp8 ragged/empty/bad table, page={ps}")
+    B, Hq, Hk, L, D = 4, 16, 2, 1000, 128
+    lens = torch.tensor([1000, 0, 37, 513], dtype=torch.int32, device="cuda")
+    q = randn((B, Hq, D), seed=60).cuda()
+    k, v = randn((B, Hk, L, D), seed=61), randn((B, Hk, L, D), seed=62)
+    _, (kp, vp, kps, vps, table) = fp8_pools(ops, k, v, ps, 63, token_major=(ps == 128))
+    bad = table.clone()
+    bad[3, 0], bad[0, 1] = -9, 10 ** 6
+    for tab in (table, bad):
+        o, lse = ops.decode_paged(q, kp, vp, tab, lens, max_seq_len=L, num_splits=3,
+                                  return_lse=True, k_scales=kps, v_scales=vps)
+        torch.cuda.synchronize()
+        to, tl = oracle.decode_paged(bits(q), kp.cpu().numpy(), vp.cpu().numpy(),
+                                     tab.cpu().numpy(), lens.cpu().numpy(), max_seq_len=L,
+                                     num_splits=3, k_scales=kps.cpu().numpy(),
+                                     v_scales=vps.cpu().numpy())
+        ref = oracle.decode(to, oracle.BF16)
+        assert np.abs(to_f32(o) - ref).max() <= TOL_FP8_ABS
+        assert (to_f32(o[1]) == 0).all() and torch.isinf(lse[1]).all() and (lse[1] < 0).all()
+        fin = np.isfinite(tl)
+        assert np.array_equal(fin, torch.isfinite(lse).cpu().numpy())
+        assert np.abs(to_f32(lse)[fin] - tl[fin]).max() <= TOL_LSE_ABS

@@ -11,8 +11,9 @@ checks the result against the CPU oracle at the contract's tolerances:
 * split-K decode (neptune_decode_splitk): bf16 and fp8 KV, GQA groups 1-16,
   ragged L, explicit and library-chosen split counts, fp8 scale blocks of
   32, 64 and 128 tokens;
-* paged decode (neptune_decode_paged): page sizes 32-256, both pool
-  layouts, ragged lengths including empty sequences.
+* paged decode (neptune_decode_paged, neptune_decode_paged_fp8): page sizes
+  32-256, both pool layouts, bf16 and fp8 pools, ragged lengths including
+  empty sequences.
 """
 
 import numpy as np
@@ -171,19 +172,35 @@ def test_paged_decode_sweep(ops, i):
     lens = [int(x) for x in rng.integers(0, L + 1, size=B)]
     token_major = bool(rng.integers(0, 2))
     splits = int(rng.choice([0, 2, 5]))
+    fp8 = bool(rng.integers(0, 2))
     _log(f"case: paged sweep B={B} Hq={Hq} Hk={Hk} page={ps} L={L} lens={lens} "
-         f"token_major={token_major} splits={splits}")
+         f"token_major={token_major} splits={splits} fp8={fp8}")
     q = randn((B, Hq, 128), seed=3000 + i)
     k = randn((B, Hk, L, 128), seed=3100 + i)
     v = randn((B, Hk, L, 128), seed=3200 + i)
+    scales = {}
+    if fp8:
+        # one scale per page: quantise with the page as the scale block and
+        # carry block j of sequence b to page table[b, j]
+        k, ks = (t.cpu() for t in ops.kv_quantize_fp8(k.cuda(), scale_block=ps))
+        v, vs = (t.cpu() for t in ops.kv_quantize_fp8(v.cuda(), scale_block=ps))
     kp, table = _paginate(k, ps, np.random.default_rng(3300 + i), token_major)
     vp, _ = _paginate(v, ps, np.random.default_rng(3300 + i), token_major)
+    if fp8:
+        for name, sc in (("k_scales", ks), ("v_scales", vs)):
+            pool = torch.ones((kp.shape[0], Hk), dtype=torch.float32)
+            tab = table.cpu().long()
+            for b in range(B):
+                pool[tab[b]] = sc[b].t()
+            scales[name] = pool.cuda()
     sl = torch.tensor(lens, dtype=torch.int32)
     o, lse = ops.decode_paged(q.cuda(), kp, vp, table, sl.cuda(), max_seq_len=L,
-                              num_splits=splits, return_lse=True)
+                              num_splits=splits, return_lse=True, **scales)
     torch.cuda.synchronize()
-    ro, rl = oracle.decode_paged(bits(q), bits(kp), bits(vp), table.cpu().numpy(), sl.numpy(),
-                                 max_seq_len=L, num_splits=splits)
+    pool_np = (lambda t: t.cpu().numpy()) if fp8 else bits
+    ro, rl = oracle.decode_paged(bits(q), pool_np(kp), pool_np(vp), table.cpu().numpy(),
+                                 sl.numpy(), max_seq_len=L, num_splits=splits,
+                                 **{n: t.cpu().numpy() for n, t in scales.items()})
     ref = oracle.decode(ro, oracle.BF16)
-    assert max_abs(to_f32(o), ref) <= TOL_BF16_ABS
+    assert max_abs(to_f32(o), ref) <= (TOL_FP8_ABS if fp8 else TOL_BF16_ABS)
     _lse_close(to_f32(lse), rl)

@@ -293,7 +293,7 @@ def _paginate(kv, ps, rng, token_major=False, spare=3):
     per = -(-L // ps)
     npages = B * per + spare
     ids = rng.permutation(npages)[: B * per].reshape(B, per).astype(np.int32)
-    pool = np.zeros((npages, ps, Hk, D) if token_major else (npages, Hk, ps, D), np.uint16)
+    pool = np.zeros((npages, ps, Hk, D) if token_major else (npages, Hk, ps, D), kv.dtype)
     for b in range(B):
         for j in range(per):
             blk = kv[b, :, j * ps:(j + 1) * ps]
@@ -348,6 +348,81 @@ def test_decode_paged_ragged_empty_and_clamped():
     fix[2, 0] = 0
     o3, _ = oracle.decode_paged(q, kp, vp, fix, lens, max_seq_len=L, num_splits=2)
     assert np.array_equal(o2, o3)
+
+
+def _page_scales(scales, ids, npages, rng):
+    """Per-(page, kv head) scales [npages, Hk] from per-block scales
+    [B, Hk, per] (block j of sequence b lives in page ids[b, j]); pages no
+    sequence uses get unrelated scales, so a misread shows."""
+    B, Hk, per = scales.shape
+    pool = rng.uniform(0.5, 2.0, size=(npages, Hk)).astype(np.float32)
+    for b in range(B):
+        for j in range(per):
+            pool[ids[b, j]] = scales[b, :, j]
+    return pool
+
+
+@pytest.mark.parametrize("token_major", [False, True])
+def test_decode_paged_fp8_equals_contiguous(token_major):
+    """fp8 pools with one scale per (page, kv head) read the same codes and
+    scales, in the same split layout, as the contiguous fp8 decode whose
+    scale block is the page: bit-identical output and lse. A scale moved to
+    another page changes the result."""
+    B, Hq, Hk, L, D, ps = 2, 8, 2, 640, 32, 64
+    q = bits(randn((B, Hq, D), seed=70))
+    kc, ks = oracle.kv_quantize_fp8(bits(randn((B, Hk, L, D), seed=71)), scale_block=ps)
+    vc, vs = oracle.kv_quantize_fp8(bits(randn((B, Hk, L, D), seed=72)), scale_block=ps)
+    kp, tab = _paginate(kc, ps, np.random.default_rng(9), token_major)
+    vp, _ = _paginate(vc, ps, np.random.default_rng(9), token_major)
+    npages = kp.shape[0]
+    kps = _page_scales(ks, tab, npages, np.random.default_rng(10))
+    vps = _page_scales(vs, tab, npages, np.random.default_rng(11))
+    lens = np.full(B, L, np.int32)
+    d = oracle.decode_splitk(q, kc, vc, oracle.FP8, ks, vs, num_splits=3, scale_block=ps)
+    o1, l1 = oracle.decode_paged(q, kp, vp, tab, lens, max_seq_len=L, num_splits=3,
+                                 k_scales=kps, v_scales=vps)
+    assert np.array_equal(d[0], o1) and np.array_equal(d[1], l1)
+    moved = kps.copy()
+    moved[tab[1, 2]] *= 1.5
+    o2, _ = oracle.decode_paged(q, kp, vp, tab, lens, max_seq_len=L, num_splits=3,
+                                k_scales=moved, v_scales=vps)
+    assert not np.array_equal(o1, o2)
+
+
+def test_decode_paged_fp8_ragged_empty_and_clamped():
+    B, Hq, Hk, L, D, ps = 3, 4, 2, 256, 32, 64
+    q = bits(randn((B, Hq, D), seed=73))
+    kc, ks = oracle.kv_quantize_fp8(bits(randn((B, Hk, L, D), seed=74)), scale_block=ps)
+    vc, vs = oracle.kv_quantize_fp8(bits(randn((B, Hk, L, D), seed=75)), scale_block=ps)
+    kp, tab = _paginate(kc, ps, np.random.default_rng(12))
+    vp, _ = _paginate(vc, ps, np.random.default_rng(12))
+    kps = _page_scales(ks, tab, kp.shape[0], np.random.default_rng(13))
+    vps = _page_scales(vs, tab, kp.shape[0], np.random.default_rng(14))
+    lens = np.array([200, 0, 37], np.int32)
+    o, lse = oracle.decode_paged(q, kp, vp, tab, lens, max_seq_len=L, num_splits=2,
+                                 k_scales=kps, v_scales=vps)
+    kd = oracle.decode(kc, oracle.FP8) * np.repeat(ks, ps, axis=2)[..., None]
+    vd = oracle.decode(vc, oracle.FP8) * np.repeat(vs, ps, axis=2)[..., None]
+    qf = oracle.decode(q, oracle.BF16)
+    for b, n in ((0, 200), (2, 37)):
+        ex, exl = oracle.attn_exact(qf[b][None, :, None], kd[b][None, :, :n].astype(np.float32),
+                                    vd[b][None, :, :n].astype(np.float32), oracle.F32)
+        got = oracle.decode(o[b], oracle.BF16)
+        assert np.abs(got - ex[0, :, 0]).max() <= 2e-2 * np.abs(ex).max()
+        assert np.abs(lse[b] - exl[0, :, 0]).max() <= 1e-4
+    assert (oracle.decode(o[1], oracle.BF16) == 0).all() and np.isneginf(lse[1]).all()
+    # entries outside the pool read the nearest page of the pool, scale included
+    bad = tab.copy()
+    bad[2, 0] = kp.shape[0] + 5
+    o2, _ = oracle.decode_paged(q, kp, vp, bad, lens, max_seq_len=L, num_splits=2,
+                                k_scales=kps, v_scales=vps)
+    fix = tab.copy()
+    fix[2, 0] = kp.shape[0] - 1
+    o3, _ = oracle.decode_paged(q, kp, vp, fix, lens, max_seq_len=L, num_splits=2,
+                                k_scales=kps, v_scales=vps)
+    assert np.array_equal(o2, o3)
+    with pytest.raises(ValueError):
+        oracle.decode_paged(q, kp, vp, tab, lens, max_seq_len=L)
 
 
 def test_decode_fp8_equals_dequantised_exact():
