@@ -40,13 +40,15 @@ constexpr int DH = 128;     // head_dim covered by the decode kernels
 struct DecArgs {
   const uint16_t *q;
   const void *k, *v;
+  // fp8 scales: [B, Hk, nsb] per sb-token block; paged, [npages, Hk]
   const float *ksc, *vsc;
   float *part_o, *part_ml;
   int32_t Hq, Hk, group, L, chunk, splits, nsb, sb;
   float scale2;
-  // paged KV (decode_partial_ring<true>): token t of sequence b lives in page
-  // btab[b * maxp + t / ps], at element offset page * k_ps[0] + head * k_ps[1]
-  // + (t % ps) * tok (the same for V with v_ps); seqlens[b] tokens
+  // paged KV (decode_partial_ring<true>, decode_partial_ring8<true>): token t
+  // of sequence b lives in page btab[b * maxp + t / ps], at element offset
+  // page * k_ps[0] + head * k_ps[1] + (t % ps) * tok (the same for V with
+  // v_ps); seqlens[b] tokens
   const int32_t *btab, *seqlens;
   int32_t ps, maxp, npages, tok;
   int64_t k_ps[2], v_ps[2];
@@ -334,7 +336,9 @@ __global__ __launch_bounds__(RT) void decode_partial_ring(DecArgs a) {
 // registers (exact); the per-(token block) K scale folds into the score
 // scale and the V scale into P before its bf16 rounding. 32-token steps
 // never straddle a scale block (the block is a multiple of 32 and every
-// wave range starts on a 32-token boundary).
+// wave range starts on a 32-token boundary). PAGED: the pools are addressed
+// through the block table as in decode_partial_ring<true>, and the page is
+// the scale block (one K and one V scale per page and kv head).
 //   K tile: 16-byte unit u of row r at u ^ ((r >> 1) & 7); a lane reads the
 //           16 codes of head_dim 64 sp + 16 G .. +15 (two MFMA k-steps).
 //   V tile: same layout; V^T comes from ds_read_b64_tr_b8, whose source
