@@ -133,7 +133,7 @@ def bench_decode_paged(ops, torch, steps, warmup, page_size=64, fp8=False):
     [pages, Hkv, page_size, D]). fp8 pages are head-major
     [pages, Hkv, page_size, D], hold finite positive E4M3 codes and one scale
     per (page, kv head): a token-major fp8 page leaves each kv head only a
-    128-byte run per token, which HBM serves at about 0.61 of peak against
+    128-byte run per token, which HBM serves at about 0.66 of peak against
     0.73 for head-major pages."""
     B, Hq, Hk, L, D, splits = 16, 32, 8, 32768, 128, 16
     per = L // page_size

@@ -54,6 +54,28 @@ struct DecArgs {
   int64_t k_ps[2], v_ps[2];
 };
 
+// Work-group -> (batch, kv head, split). Contiguous KV: split fastest, so
+// neighbouring work-groups stream neighbouring ranges of one head. Paged KV:
+// kv head fastest, so the work-groups reading the heads of the same tokens
+// run together; in a token-major pool ([pages, page, Hkv, D]) those heads
+// share every token's row, and fp8 decode over such a pool measured 7%
+// faster (bf16 1%) with this order, while contiguous fp8 decode measured 1%
+// slower with it.
+template <bool PAGED>
+__device__ inline void grid_item(const DecArgs &a, int id, int *b, int *hk, int *split) {
+  if (PAGED) {
+    *hk = id % a.Hk;
+    const int rest = id / a.Hk;
+    *split = rest % a.splits;
+    *b = rest / a.splits;
+  } else {
+    *split = id % a.splits;
+    const int bk = id / a.splits;
+    *b = bk / a.Hk;
+    *hk = bk % a.Hk;
+  }
+}
+
 // bf16 bits of 4 E4M3 codes packed in one dword -> two dwords of bf16 pairs
 // (v_cvt_scalef32_pk_bf16_fp8 with scale 1: every E4M3 value is a bf16 value,
 // so the widening is exact)
@@ -88,9 +110,9 @@ __global__ __launch_bounds__(RT) void decode_partial_ring(DecArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, G = lane >> 4;  // MFMA column (query head) / lane group
   const int id = blockIdx.x;
-  const int split = id % a.splits;
-  const int bk = id / a.splits;  // batch * Hk + kv head
-  const int b = bk / a.Hk, hk = bk % a.Hk;
+  int split, b, hk;
+  grid_item<PAGED>(a, id, &b, &hk, &split);
+  const int bk = b * a.Hk + hk;  // batch * Hk + kv head
   const int Gq = a.group;
   // this sequence's length (paged: its own; out-of-range values clamped)
   const int Lb = PAGED ? min(max(a.seqlens[b], 0), a.L) : a.L;
@@ -362,9 +384,9 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, G = lane >> 4;
   const int id = blockIdx.x;
-  const int split = id % a.splits;
-  const int bk = id / a.splits;
-  const int b = bk / a.Hk, hk = bk % a.Hk;
+  int split, b, hk;
+  grid_item<PAGED>(a, id, &b, &hk, &split);
+  const int bk = b * a.Hk + hk;  // batch * Hk + kv head
   const int Gq = a.group;
   // this sequence's length (paged: its own; out-of-range values clamped)
   const int Lb = PAGED ? min(max(a.seqlens[b], 0), a.L) : a.L;
