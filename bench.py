@@ -195,24 +195,24 @@ def bench_scan(ops, torch, steps, warmup, rotate=2):
     return "config4 Mamba-1 selective scan", wall, ev, nbytes
 
 
-def cpu_baseline_prefill(res, budget_s=15.0, max_heads=32):
-    """CPU oracle (HTile policy, OpenMP) on whole (batch 0, head h) slices of
-    the same inputs until the time budget is spent."""
+def cpu_baseline_prefill(res, budget_s=15.0, max_slices=64):
+    """CPU oracle (HTile policy, OpenMP) on whole (batch, head) slices of the
+    same inputs, in order, until the time budget is spent."""
     import numpy as np
     import torch
 
     import oracle
 
-    S, D = res["q"].shape[2], res["q"].shape[3]
+    B, H, S, D = res["q"].shape
     per_head = prefill_flops(1, 1, S, D)
 
     def b16(t):
         return t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
 
     done, elapsed = 0, 0.0
-    while elapsed < budget_s and done < max_heads:
-        h = done
-        sl = (slice(0, 1), slice(h, h + 1))
+    while elapsed < budget_s and done < min(max_slices, B * H):
+        b, h = divmod(done, H)
+        sl = (slice(b, b + 1), slice(h, h + 1))
         qs, ks, vs = b16(res["q"][sl]), b16(res["k"][sl]), b16(res["v"][sl])
         t0 = time.perf_counter()
         oracle.attn_fwd(qs, ks, vs, oracle.BF16, causal=True)
@@ -223,7 +223,7 @@ def cpu_baseline_prefill(res, budget_s=15.0, max_heads=32):
         "unit": "TFLOP/s",
         "cores": oracle.num_threads(),
         "kind": "port",
-        "sample": f"{done} of 128 (batch, head) slices of the same causal prefill "
+        "sample": f"{done} of {B * H} (batch, head) slices of the same causal prefill "
                   f"({elapsed:.1f} s of CPU oracle time)",
     }
 
