@@ -56,6 +56,7 @@ constexpr int HD = 128;
 constexpr int NT = 256;
 constexpr int TILE = BN * HD * 2;  // bytes per K or V tile (16 KiB)
 constexpr float kSlack = 8.0f;     // lazy-rescale threshold (log2 units)
+constexpr float kSumCap = 256.0f;  // 2^kSlack: a lane's block sum at most this skips the max
 
 // Wave w copies rows [16w, 16w+16) of a 64 x 128 tile (four 1 KiB chunks of
 // four rows) straight into LDS. Full blocks take a wave-uniform base pointer
@@ -392,42 +393,59 @@ __global__ __launch_bounds__(NT, STAGES == 3 ? 1 : 2) void attn_fwd_d128(AttnArg
           for (int r = 0; r < 16; ++r)
             if (32 * kb + 8 * (r >> 2) + (r & 3) > lim) s[kb][r] = -INFINITY;
       }
-      float mx = -INFINITY;
+      // p = 2^(s sc - m) for the block, packed for P.V, and the lane's sum
+      float rs;
+      u32x4 pf[4];
+      auto expo = [&]() {
+        const float nm = -m;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+        for (int c = 0; c < 4; ++c) {
+          const int kb = c >> 1, hh = c & 1;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-      mx = pair_max(mx);
+          for (int i = 0; i < 4; ++i) {
+            const float p0 = fast_exp2(fmaf(s[kb][8 * hh + 2 * i], sc, nm));
+            const float p1 = fast_exp2(fmaf(s[kb][8 * hh + 2 * i + 1], sc, nm));
+            rs = c + i == 0 ? p0 : rs + p0;  // the sum from 0.0 without its first add
+            rs += p1;
+            pf[c][i] = E::pack2(p0, p1);
+          }
+        }
+      };
       // Lazy rescaling: the running max m only moves when a row's block max
       // exceeds it by more than kSlack (a factor 2^kSlack); in between,
       // p = 2^(s - m) <= 2^kSlack, which the fp32 sums hold exactly as well
       // and whose 16-bit rounding is relative, so results differ from a
       // rescale at every block by rounding only.
-      const float m_blk = mx * sc;
-      if (__any(m_blk > m + kSlack)) {
-        const float m_new = fmaxf(m, m_blk);
-        const float alpha = fast_exp2(m - m_new);
-        lsum *= alpha;
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[nb][r] *= alpha;
-        m = m_new;
+      // The block max is only formed when it can matter. Past a query block's
+      // first key block, p is first taken against m as it stands: when every
+      // lane's sum of its p stays within 2^kSlack, so does every p, and m
+      // keeps. Otherwise (a p above 2^kSlack, an overflow to inf, a NaN, or
+      // only a large sum) the max is formed, m moves if it must, and p is
+      // taken again. The first key block always forms it (m starts at -FLT_MAX).
+      bool full = jb == 0;
+      if (!full) {
+        expo();
+        full = __any(!(rs <= kSumCap));
       }
-      const float nm = -m;
-      float rs = 0.0f;
-      u32x4 pf[4];
+      if (full) {
+        float mx = -INFINITY;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int kb = c >> 1, hh = c & 1;
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p0 = fast_exp2(fmaf(s[kb][8 * hh + 2 * i], sc, nm));
-          const float p1 = fast_exp2(fmaf(s[kb][8 * hh + 2 * i + 1], sc, nm));
-          rs += p0;
-          rs += p1;
-          pf[c][i] = E::pack2(p0, p1);
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+        mx = pair_max(mx);
+        const float m_blk = mx * sc;
+        if (__any(m_blk > m + kSlack)) {
+          const float m_new = fmaxf(m, m_blk);
+          const float alpha = fast_exp2(m - m_new);
+          lsum *= alpha;
+#pragma unroll
+          for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[nb][r] *= alpha;
+          m = m_new;
         }
+        expo();
       }
       lsum += rs;
 
