@@ -35,6 +35,49 @@ constexpr int STEP = 32;    // tokens per wave step
 // which fp32 sums hold exactly as well and whose bf16 rounding is relative,
 // so results differ from a rescale at every step by rounding only.
 constexpr float kSlack = 8.0f;
+
+// One step's p = 2^(s - m) and the lane's sum rs, with the lazy rescale: the
+// running max m moves only when a row's step max passes it by more than
+// kSlack, rescaling O and l. Past the first step p is first taken against m
+// as it stands; when every lane's sum stays within 2^kSlack, so does every
+// p, and the step max is not needed. Otherwise (a p above 2^kSlack, an
+// overflow, a NaN, or only a large sum) the max is formed, m moves if it
+// must, and p is taken again. The first step always forms it (m starts at
+// -FLT_MAX). A row's four lanes (lane ^ 16, ^ 32) decide together.
+__device__ inline void softmax_step(const f32x4 (&s)[2], bool first, float &m, float &lsum,
+                                    f32x4 (&oacc)[8], float (&p)[8], float &rs) {
+  auto expo = [&]() {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      p[j] = fast_exp2(s[j >> 2][j & 3] - m);
+      rs = j == 0 ? p[j] : rs + p[j];
+    }
+  };
+  bool full = first;
+  if (!full) {
+    expo();
+    full = __any(!(rs <= 256.0f));  // 2^kSlack
+  }
+  if (full) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kb][r]);
+    mx = max_xor32(max_xor16(mx));
+    if (__any(mx > m + kSlack)) {
+      const float m_new = fmaxf(m, mx);
+      const float alpha = fast_exp2(m - m_new);
+      m = m_new;
+      lsum *= alpha;
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) oacc[mb][r] *= alpha;
+    }
+    expo();
+  }
+}
 constexpr int DH = 128;     // head_dim covered by the decode kernels
 
 struct DecArgs {
@@ -269,31 +312,8 @@ __global__ __launch_bounds__(RT) void decode_partial_ring(DecArgs a) {
         for (int r = 0; r < 4; ++r)
           if (t + 16 * kb + 4 * G + r >= t1) s[kb][r] = -INFINITY;
     }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kb][r]);
-    mx = max_xor32(max_xor16(mx));
-    // lazy rescale: the running max moves only past a 2^kSlack margin
-    if (__any(mx > m + kSlack)) {
-      const float m_new = fmaxf(m, mx);
-      const float alpha = fast_exp2(m - m_new);
-      m = m_new;
-      lsum *= alpha;
-#pragma unroll
-      for (int mb = 0; mb < 8; ++mb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) oacc[mb][r] *= alpha;
-    }
-    float rs = 0.0f;
-    float p[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float e = fast_exp2(s[j >> 2][j & 3] - m);
-      rs += e;
-      p[j] = e;
-    }
+    float rs, p[8];
+    softmax_step(s, i == 0, m, lsum, oacc, p, rs);
     lsum += rs;
     // P^T: k-slot 8 G + j holds key 4 G + j (j < 4) or 16 + 4 G + j - 4
     u32x4 pf;
@@ -586,31 +606,8 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
         for (int r = 0; r < 4; ++r)
           if (t + 16 * kb + 4 * G + r >= t1) s[kb][r] = -INFINITY;
     }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kb][r]);
-    mx = max_xor32(max_xor16(mx));
-    // lazy rescale: the running max moves only past a 2^kSlack margin
-    if (__any(mx > m + kSlack)) {
-      const float m_new = fmaxf(m, mx);
-      const float alpha = fast_exp2(m - m_new);
-      m = m_new;
-      lsum *= alpha;
-#pragma unroll
-      for (int mb = 0; mb < 8; ++mb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) oacc[mb][r] *= alpha;
-    }
-    float rs = 0.0f;
-    float p[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float e = fast_exp2(s[j >> 2][j & 3] - m);
-      rs += e;
-      p[j] = e;
-    }
+    float rs, p[8];
+    softmax_step(s, i == 0, m, lsum, oacc, p, rs);
     lsum += rs;
     u32x4 pf;
 #pragma unroll
