@@ -373,6 +373,14 @@ bool attn_supported(const AttnLaunch &a, const char **why) {
     *why = "sequence or batch*heads too large for one launch";
     return false;
   }
+  // a dispatch covers at most 2^32 - 1 work-items: one 256-thread work-group
+  // per 128 query rows and (batch, head) (the most any 16-bit path launches),
+  // one 64-thread work-group per 64 rows for fp32
+  const int64_t rows = a.dtype == 0 ? F32_BM : BM, thr = a.dtype == 0 ? 64 : NTHR;
+  if ((a.seq_q + rows - 1) / rows * (a.batch * a.heads_q) * thr > (int64_t)0xffffffff) {
+    *why = "batch*heads*seq_q too large for one launch";
+    return false;
+  }
   return true;
 }
 

@@ -37,11 +37,12 @@
 //     produces (HTilePasses.cpp:122-140) -- as head_dim rows of 64 keys, and
 //     forms the A operand with ds_read_b64_tr_b16 as V^T is formed.
 //
-// Work-groups: each runs two query blocks of one head, q0 = nqb-1-p and
-// q1 = p, back to back; the K/V stream simply continues from q0's last key
-// block into q1's first, so q1's tiles (and its Q^T) load while q0 drains.
-// Under the causal mask the pair's key-block count is the same for every p,
-// so all work-groups carry equal work (no tail of heavy stragglers).
+// Work-groups: without the causal mask each runs two query blocks of one
+// head, q0 = nqb-1-p and q1 = p, back to back; the K/V stream simply
+// continues from q0's last key block into q1's first, so q1's tiles load
+// while q0 drains, and a launch has half as many prologues. Under the causal
+// mask each runs one query block, and the grid dispatches the heaviest
+// blocks first, so the end of the launch is filled by the lightest ones.
 #include "attn_args.h"
 #include "device_common.h"
 #include "kernels.h"
@@ -161,22 +162,49 @@ __device__ inline float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Work-group -> (batch*head, pair of query blocks). A work-group runs query
-// blocks q0 = nqb-1-p and q1 = p of one head; under the causal mask their
-// key-block counts add up to the same total for every p, so all work-groups
-// carry equal work and the grid has no tail of heavy stragglers. With
-// batch*heads a multiple of 8, work-group id % 8 is the XCD it is dispatched
-// to and each XCD walks its own heads in order, so the K/V of the heads in
+// Work-group -> (batch*head, query blocks q0, q1; q1 == q0 for one block).
+// With batch*heads a multiple of 8, work-group id % 8 is the XCD it is
+// dispatched to, and each XCD walks its own heads, so the K/V of the heads in
 // flight on an XCD stay in that XCD's L2.
-__device__ inline void map_block(const AttnArgs &a, int npair, int id, int *pair, int *bh) {
-  if ((a.BH & 7) == 0) {
-    const int x = id & 7, k = id >> 3;
-    const int t = k / npair;
-    *bh = x + 8 * t;
-    *pair = k - t * npair;
+// - No mask: pair p of a head runs q0 = nqb-1-p and q1 = p; each XCD walks
+//   its heads in order, all pairs of one head together.
+// - Causal: one block per work-group. Each XCD takes its heads four at a
+//   time (a window) and runs a window's blocks from the heaviest (the last
+//   query block, which sees every key block) to the lightest, the four heads
+//   interleaved. Work-groups are dispatched in id order as slots free up, so
+//   the last ones a slot takes are the shortest, and the launch's end is
+//   not held up by one long work-group per slot (the longest-first rule).
+template <bool CAUSAL>
+__device__ inline void map_block(const AttnArgs &a, int npair, int id, int *q0, int *q1,
+                                 int *bh) {
+  if constexpr (CAUSAL) {
+    int q;
+    if ((a.BH & 7) == 0) {
+      const int x = id & 7, k = id >> 3, hx = a.BH >> 3;
+      const int G = hx < 4 ? hx : 4;
+      const int win = k / (G * a.nqb);
+      const int gh = min(G, hx - win * G);  // heads in this (possibly last) window
+      const int r = k - win * G * a.nqb;
+      q = a.nqb - 1 - r / gh;
+      *bh = x + 8 * (win * G + r % gh);
+    } else {
+      *bh = id % a.BH;
+      q = a.nqb - 1 - id / a.BH;
+    }
+    *q0 = *q1 = q;
   } else {
-    *bh = id % a.BH;
-    *pair = id / a.BH;
+    int pair;
+    if ((a.BH & 7) == 0) {
+      const int x = id & 7, k = id >> 3;
+      const int t = k / npair;
+      *bh = x + 8 * t;
+      pair = k - t * npair;
+    } else {
+      *bh = id % a.BH;
+      pair = id / a.BH;
+    }
+    *q0 = a.nqb - 1 - pair;
+    *q1 = pair;
   }
 }
 
@@ -195,15 +223,16 @@ __global__ __launch_bounds__(NT, STAGES == 3 ? 1 : 2) void attn_fwd_d128(AttnArg
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane & 31, g = lane >> 5;
 
-  int pair, bh;
-  map_block(a, npair, blockIdx.x, &pair, &bh);
+  int q0, q1, bh;
+  map_block<CAUSAL>(a, npair, blockIdx.x, &q0, &q1, &bh);
   const int b = bh / a.Hq, h = bh - b * a.Hq, hk = h / a.group;
   const uint16_t *qp = (const uint16_t *)a.q + b * a.qs0 + h * a.qs1;
   const uint16_t *kp = (const uint16_t *)a.k + b * a.ks0 + hk * a.ks1;
   const uint16_t *vp = (const uint16_t *)a.v + b * a.vs0 + hk * a.vs1;
 
-  // the two query blocks (the heavier first); a lone middle block has n1 = 0
-  const int qbs[2] = {a.nqb - 1 - pair, pair};
+  // the query blocks (the heavier first); one block (causal, or the middle
+  // block of an odd count) has n1 = 0
+  const int qbs[2] = {q0, q1};
   const bool two = qbs[1] != qbs[0];
   int nkb[2], nkw[2];  // key blocks per query block: work-group, this wave
 #pragma unroll
@@ -521,11 +550,12 @@ __global__ __launch_bounds__(NT, STAGES == 3 ? 1 : 2) void attn_fwd_d128(AttnArg
 template <class E, int STAGES, bool KT>
 void launch_t(const AttnArgs &a, bool causal, hipStream_t s) {
   const int npair = (a.nqb + 1) / 2;
-  const dim3 grid((unsigned)(npair * a.BH));
   if (causal)
-    hipLaunchKernelGGL((attn_fwd_d128<E, true, STAGES, KT>), grid, dim3(NT), 0, s, a, npair);
+    hipLaunchKernelGGL((attn_fwd_d128<E, true, STAGES, KT>), dim3((unsigned)(a.nqb * a.BH)),
+                       dim3(NT), 0, s, a, npair);
   else
-    hipLaunchKernelGGL((attn_fwd_d128<E, false, STAGES, KT>), grid, dim3(NT), 0, s, a, npair);
+    hipLaunchKernelGGL((attn_fwd_d128<E, false, STAGES, KT>), dim3((unsigned)(npair * a.BH)),
+                       dim3(NT), 0, s, a, npair);
 }
 
 template <class E, bool KT>

@@ -179,6 +179,7 @@ def test_attn_null_and_stride_errors(lib):
     (dict(pipeline_stages=1, dtype=_abi.DTYPE_F32), _abi.ERR_UNSUPPORTED),
     (dict(k_dim_order=1, head_dim=64), _abi.ERR_UNSUPPORTED),
     (dict(k_dim_order=1, seq_kv=100), _abi.ERR_UNSUPPORTED),         # contiguous K^T row of 100
+    (dict(batch=8192, heads_q=2048, heads_kv=2048, seq_q=256), _abi.ERR_UNSUPPORTED),  # 2^33 work-items
     (dict(pipeline_stages=2, dtype=_abi.DTYPE_F32, head_dim=64), _abi.ERR_NO_DEVICE),
     (dict(pipeline_stages=3, k_dim_order=1), _abi.ERR_NO_DEVICE),
     (dict(pipeline_stages=1), _abi.ERR_NO_DEVICE),
