@@ -373,6 +373,16 @@ bool attn_supported(const AttnLaunch &a, const char **why) {
     *why = "sequence or batch*heads too large for one launch";
     return false;
   }
+  // The head_dim-128 kernel addresses a full K or V tile from a per-block
+  // base plus per-lane 32-bit byte offsets: up to row 63 of a 64-key tile
+  // (row 127 of a 128-row head_dim-major K tile) and 256 bytes into it.
+  if (d128) {
+    const int64_t klast = a.k_dim_order ? 127 : 63;
+    if (klast * a.ks[2] * 2 + 256 > (int64_t)0xffffffff || 63 * a.vs[2] * 2 + 256 > (int64_t)0xffffffff) {
+      *why = "K or V row stride too large: a 64-key tile must span less than 4 GiB";
+      return false;
+    }
+  }
   // a dispatch covers at most 2^32 - 1 work-items: one 256-thread work-group
   // per 128 query rows and (batch, head) (the most any 16-bit path launches),
   // one 64-thread work-group per 64 rows for fp32

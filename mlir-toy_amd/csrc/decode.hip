@@ -79,6 +79,7 @@ __device__ inline void softmax_step(const f32x4 (&s)[2], bool first, float &m, f
   }
 }
 constexpr int DH = 128;     // head_dim covered by the decode kernels
+constexpr int64_t kMaxSplits = 16384;  // combine: one fp32 weight per split in 64 KiB of LDS
 
 struct DecArgs {
   const uint16_t *q;
@@ -832,6 +833,11 @@ bool decode_supported(const DecodeLaunch &a, const char **why) {
   if (a.seq_kv > (int64_t)1 << 30 ||
       a.batch * a.heads_kv * a.splits > (int64_t)1 << 30) {
     *why = "decode shape too large for one launch";
+    return false;
+  }
+  // the combine keeps one fp32 weight per split in LDS (64 KiB at most)
+  if (a.splits > kMaxSplits) {
+    *why = "decode supports at most 16384 splits";
     return false;
   }
   return true;

@@ -7,7 +7,7 @@ passes device pointers and streams to it, and offers the HTile front end
 """
 
 from ._abi import (  # noqa: F401
-    DEFAULT_LIBRARY_ENV,
+    LIBRARY_ENV,
     NeptuneError,
     NeptuneHipError,
     NeptuneInvalidArgument,
@@ -20,7 +20,7 @@ from ._abi import (  # noqa: F401
 )
 
 __all__ = [
-    "DEFAULT_LIBRARY_ENV",
+    "LIBRARY_ENV",
     "NeptuneError",
     "NeptuneHipError",
     "NeptuneInvalidArgument",

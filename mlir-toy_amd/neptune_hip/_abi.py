@@ -1,12 +1,11 @@
 """ctypes view of include/neptune_hip.h and the library locator.
 
-The locator follows the resolution order of the reference's plugin finder
-(src/neptune_mlir/plugin.py:28-55): explicit path, then an environment
-variable, then the package's ``_native`` directory, then ``<repo>/build`` and
-``<cwd>/build``. Failures of the C-ABI map onto the exception classes the
-reference raises for the same situations: ``NotImplementedError`` for valid
-requests the backend does not cover (translators/common.py:187-197) and
-``RuntimeError`` for toolchain/runtime failures (common.py:217-224).
+The locator searches where the reference's plugin finder searches
+(src/neptune_mlir/plugin.py:28-55), in the same order. Failures of the
+C-ABI map onto the exception classes the reference raises for the same
+situations: ``NotImplementedError`` for valid requests the backend does not
+cover (translators/common.py:187-197) and ``RuntimeError`` for
+toolchain/runtime failures (common.py:217-224).
 """
 
 from __future__ import annotations
@@ -14,9 +13,10 @@ from __future__ import annotations
 import ctypes
 import os
 from pathlib import Path
+from typing import Iterator
 
-DEFAULT_LIBRARY_ENV = "NEPTUNE_HIP_LIB"
-LIBRARY_PATTERNS = ("libneptune_hip.so",)
+LIBRARY_ENV = "NEPTUNE_HIP_LIB"
+LIBRARY_FILE = "libneptune_hip.so"
 
 ABI_VERSION = 1
 
@@ -153,42 +153,23 @@ _STATUS_CLASSES = {
 }
 
 
-def _find_in_dir(directory: Path) -> Path | None:
-    for pattern in LIBRARY_PATTERNS:
-        matches = sorted(directory.glob(pattern))
-        if matches:
-            return matches[0]
-    return None
-
-
-def _candidate_dirs() -> list[Path]:
-    pkg_dir = Path(__file__).resolve().parent
-    repo_root = pkg_dir.parents[1]
-    return [pkg_dir / "_native", repo_root / "build", Path.cwd() / "build"]
+def _library_candidates(explicit) -> Iterator[Path]:
+    """Files that may hold the backend, the caller's choice first: the
+    explicit path, the LIBRARY_ENV variable, the library this package was
+    built with, then a development build under the repository or the
+    working directory (the reference's plugin search order,
+    src/neptune_mlir/plugin.py:28-55)."""
+    for given in (explicit, os.environ.get(LIBRARY_ENV)):
+        if given:
+            yield Path(given).expanduser()
+    package = Path(__file__).resolve().parent
+    for where in (package / "_native", package.parents[1] / "build", Path.cwd() / "build"):
+        yield where / LIBRARY_FILE
 
 
 def find_library_path(explicit: str | os.PathLike[str] | None = None) -> Path | None:
-    """Resolve libneptune_hip.so.
-
-    Resolution order:
-    1. Explicit path argument.
-    2. NEPTUNE_HIP_LIB environment variable.
-    3. Package directory: neptune_hip/_native.
-    4. Development build dirs: <repo>/build and <cwd>/build.
-    """
-    candidates: list[Path] = []
-    if explicit:
-        candidates.append(Path(explicit).expanduser())
-    env_path = os.environ.get(DEFAULT_LIBRARY_ENV)
-    if env_path:
-        candidates.append(Path(env_path).expanduser())
-    for candidate in candidates:
-        if candidate.is_file():
-            return candidate.resolve()
-    for directory in _candidate_dirs():
-        if directory.is_dir() and (match := _find_in_dir(directory)) is not None:
-            return match.resolve()
-    return None
+    """The first existing candidate of ``_library_candidates``, or None."""
+    return next((c.resolve() for c in _library_candidates(explicit) if c.is_file()), None)
 
 
 _LIB: ctypes.CDLL | None = None
@@ -240,7 +221,7 @@ def load_library(explicit: str | os.PathLike[str] | None = None) -> ctypes.CDLL:
     if path is None:
         raise RuntimeError(
             "libneptune_hip.so not found: build it (python -c 'import __graft_entry__ as g; "
-            f"g.build()') or set {DEFAULT_LIBRARY_ENV}"
+            f"g.build()') or set {LIBRARY_ENV}"
         )
     lib = ctypes.CDLL(str(path))
     _declare(lib)

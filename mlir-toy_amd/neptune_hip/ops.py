@@ -183,17 +183,35 @@ def decode_splitk(
     [B, Hkv, ceil(L/scale_block)] fp32. Returns o [B, Hq, D] bf16.
     """
     q3 = _as_q3(q)
-    _require_cuda(q3, k, v, k_scale, v_scale, workspace)
     fp8 = k.dtype in (torch.uint8, torch.float8_e4m3fn)
     if q3.dtype != torch.bfloat16:
         raise ValueError("decode query must be bfloat16")
     if not fp8 and k.dtype != torch.bfloat16:
         raise ValueError("decode KV must be bfloat16 or E4M3 codes")
+    if q3.dim() != 3 or k.dim() != 4:
+        raise ValueError("decode takes q [B, Hq, D] and k, v [B, Hkv, L, D]")
     if v.dtype != k.dtype or tuple(v.shape) != tuple(k.shape):
         raise ValueError("k and v must match")
+    B, _, D = q3.shape
+    Bk, Hk, L, Dk = k.shape
+    if (Bk, Dk) != (B, D):
+        raise ValueError(f"k {tuple(k.shape)} does not match q {tuple(q3.shape)} in batch or "
+                         "head_dim")
     for t in (q3, k, v):
         if not t.is_contiguous():
             raise ValueError("decode tensors must be contiguous")
+    if fp8:
+        if scale_block <= 0:
+            raise ValueError("scale_block must be positive")
+        want = (B, Hk, -(-L // scale_block))
+        for name, t in (("k_scale", k_scale), ("v_scale", v_scale)):
+            if t is None or t.dtype != torch.float32 or not t.is_contiguous() or \
+                    tuple(t.shape) != want:
+                raise ValueError(f"fp8 KV needs {name}: contiguous float32 {list(want)} "
+                                 f"(scale_block {scale_block})")
+    elif k_scale is not None or v_scale is not None:
+        raise ValueError("k_scale / v_scale apply to E4M3 KV only")
+    _require_cuda(q3, k, v, k_scale, v_scale, workspace)
     desc = _decode_desc(q3, k, num_splits, scale_block, scale,
                         _abi.DTYPE_FP8_E4M3 if fp8 else _abi.DTYPE_BF16)
     lib = load_library()
@@ -250,7 +268,6 @@ def decode_paged(
     layout. Returns o [B, Hq, D] bf16.
     """
     q3 = _as_q3(q)
-    _require_cuda(q3, k_pages, v_pages, block_table, seq_lens, workspace, k_scales, v_scales)
     fp8 = k_pages.dtype in (torch.uint8, torch.float8_e4m3fn)
     if q3.dtype != torch.bfloat16 or k_pages.dtype != v_pages.dtype or \
             not (fp8 or k_pages.dtype == torch.bfloat16):
@@ -262,14 +279,19 @@ def decode_paged(
         if t.dtype != torch.int32 or not t.is_contiguous():
             raise ValueError(f"{name} must be a contiguous int32 tensor")
     npages, Hk, psize, D = k_pages.shape
+    if q3.dim() != 3 or q3.shape[2] != D:
+        raise ValueError(f"q {tuple(q3.shape)} does not match the pools' head_dim {D}")
     if fp8:
         for name, t in (("k_scales", k_scales), ("v_scales", v_scales)):
             if t is None or t.dtype != torch.float32 or not t.is_contiguous() or \
                     tuple(t.shape) != (npages, Hk):
                 raise ValueError(f"fp8 pages need {name}: contiguous float32 [num_pages, Hkv]")
+    elif k_scales is not None or v_scales is not None:
+        raise ValueError("k_scales / v_scales apply to E4M3 pools only")
     B = q3.shape[0]
     if block_table.dim() != 2 or block_table.shape[0] != B or tuple(seq_lens.shape) != (B,):
         raise ValueError("block_table [B, max_pages] and seq_lens [B] must match q's batch")
+    _require_cuda(q3, k_pages, v_pages, block_table, seq_lens, workspace, k_scales, v_scales)
     max_pages = block_table.shape[1]
     L = int(max_seq_len) if max_seq_len is not None else max_pages * psize
     k4 = torch.empty((B, Hk, L, D), dtype=k_pages.dtype, device="meta")
@@ -339,18 +361,24 @@ def selective_scan(
     u, delta, z [batch, dim, L] and B, C [batch, d_state, L] bf16; A
     [dim, d_state], D and delta_bias [dim] fp32. Returns y [batch, dim, L] bf16.
     """
-    _require_cuda(u, delta, A, B, C, D, z, delta_bias)
     for name, t in (("u", u), ("delta", delta), ("B", B), ("C", C), ("z", z)):
         if t is not None and (t.dtype != torch.bfloat16 or not t.is_contiguous()):
             raise ValueError(f"{name} must be contiguous bfloat16")
     for name, t in (("A", A), ("D", D), ("delta_bias", delta_bias)):
         if t is not None and (t.dtype != torch.float32 or not t.is_contiguous()):
             raise ValueError(f"{name} must be contiguous float32")
+    if u.dim() != 3 or A.dim() != 2:
+        raise ValueError("selective_scan takes u [batch, dim, L] and A [dim, d_state]")
     bsz, dim, L = u.shape
     N = A.shape[1]
-    if tuple(delta.shape) != (bsz, dim, L) or tuple(B.shape) != (bsz, N, L) or \
-            tuple(C.shape) != (bsz, N, L) or tuple(A.shape) != (dim, N):
-        raise ValueError("selective_scan shape mismatch")
+    want = {"delta": (bsz, dim, L), "A": (dim, N), "B": (bsz, N, L), "C": (bsz, N, L),
+            "z": (bsz, dim, L), "D": (dim,), "delta_bias": (dim,)}
+    for name, t in (("delta", delta), ("A", A), ("B", B), ("C", C), ("z", z), ("D", D),
+                    ("delta_bias", delta_bias)):
+        if t is not None and tuple(t.shape) != want[name]:
+            raise ValueError(f"selective_scan: {name} is {tuple(t.shape)}, expected "
+                             f"{want[name]}")
+    _require_cuda(u, delta, A, B, C, D, z, delta_bias)
     y = torch.empty_like(u)
     desc = _abi.ScanDesc(bsz, dim, L, N, _abi.DTYPE_BF16, 1 if delta_softplus else 0)
     lib = load_library()

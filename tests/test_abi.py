@@ -421,11 +421,51 @@ def test_locator_order(tmp_path, monkeypatch):
     (the reference's plugin resolution order, src/neptune_mlir/plugin.py:28-55)."""
     fake = tmp_path / "libneptune_hip.so"
     fake.write_bytes(b"")
-    monkeypatch.delenv(_abi.DEFAULT_LIBRARY_ENV, raising=False)
+    monkeypatch.delenv(_abi.LIBRARY_ENV, raising=False)
     default = _abi.find_library_path()
     assert default is not None and default.parent.name == "_native"
     assert _abi.find_library_path(fake) == fake.resolve()
-    monkeypatch.setenv(_abi.DEFAULT_LIBRARY_ENV, str(fake))
+    monkeypatch.setenv(_abi.LIBRARY_ENV, str(fake))
     assert _abi.find_library_path() == fake.resolve()
-    monkeypatch.setenv(_abi.DEFAULT_LIBRARY_ENV, str(tmp_path / "missing.so"))
+    monkeypatch.setenv(_abi.LIBRARY_ENV, str(tmp_path / "missing.so"))
     assert _abi.find_library_path() == default
+
+
+@pytest.mark.parametrize("field,stride", [
+    ("k_stride", (1, 1, 34_100_000)),   # 63 rows x 68.2 MB per K row passes 2^32 bytes
+    ("v_stride", (1, 1, 34_100_000)),
+])
+def test_attn_rejects_tiles_past_32_bit_offsets(lib, field, stride):
+    """A 64-key K or V tile is addressed as a base plus 32-bit per-lane byte
+    offsets; token strides that would wrap them are UNSUPPORTED, not
+    silently read from the wrong rows."""
+    d = _attn_desc()
+    for name in ("q_stride", "k_stride", "v_stride", "o_stride"):
+        getattr(d, name)[:] = (1 << 40, 1 << 32, 128)
+    getattr(d, field)[:] = (1 << 40, 1 << 32, stride[2] // 8 * 8)
+    assert _attn(lib, d) == _abi.ERR_UNSUPPORTED
+    assert b"4 GiB" in lib.neptune_last_error()
+
+
+def test_attn_rejects_long_head_dim_major_k(lib):
+    """k_dim_order 1 spans 128 head_dim rows of seq_kv keys: seq_kv above
+    about 16.9M tokens would wrap the 32-bit offsets."""
+    L = 17_000_000
+    d = _attn_desc(k_dim_order=1, seq_kv=L, seq_q=128)
+    assert _attn(lib, d) == _abi.ERR_UNSUPPORTED
+    assert b"4 GiB" in lib.neptune_last_error()
+    if lib.neptune_device_count() == 0:
+        ok = _attn_desc(k_dim_order=1, seq_kv=16_000_000, seq_q=128)
+        assert _attn(lib, ok) == _abi.ERR_NO_DEVICE
+
+
+def test_decode_rejects_splits_past_the_combine_lds(lib):
+    """decode_combine keeps one fp32 weight per split in LDS: more than
+    16384 splits is UNSUPPORTED at validation, before any launch."""
+    L = 64 * 16385
+    d = _dec_desc(batch=1, heads_q=1, heads_kv=1, seq_kv=L, num_splits=16385)
+    assert _decode(lib, d) == _abi.ERR_UNSUPPORTED
+    assert b"16384 splits" in lib.neptune_last_error()
+    if lib.neptune_device_count() == 0:
+        d = _dec_desc(batch=1, heads_q=1, heads_kv=1, seq_kv=L, num_splits=16384)
+        assert _decode(lib, d) == _abi.ERR_NO_DEVICE
