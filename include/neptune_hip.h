@@ -175,6 +175,22 @@ NEPTUNE_API neptune_status neptune_decode_splitk(const neptune_decode_desc *desc
                                      void *workspace, size_t workspace_bytes,
                                      void *stream);
 
+/* neptune_decode_splitk without a workspace argument; it allocates nothing.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops). The
+ * split partials go to a static device scratch of 16 MiB that each GPU
+ * holds until the process ends (520 bytes per batch x heads_q x split row:
+ * config 3's 16 x 32 x 16 rows use 4.3 MB); a request that needs more
+ * returns NEPTUNE_ERR_WORKSPACE_TOO_SMALL. Every call on one GPU shares that
+ * scratch: calls that overlap on one GPU (concurrent streams, or threads
+ * enqueueing at once) race on it and must be ordered by the caller. The
+ * results equal neptune_decode_splitk's bit for bit. */
+NEPTUNE_API neptune_status neptune_decode_splitk_noalloc(const neptune_decode_desc *desc,
+                                             const void *q, const void *k,
+                                             const void *v, const float *k_scale,
+                                             const float *v_scale, void *o, float *lse,
+                                             void *stream);
+
 /* Quantise a BF16 KV tensor [batch, heads_kv, seq_kv, head_dim] to E4M3FN
  * codes with one fp32 scale per (batch, kv head, scale_block tokens):
  * scale = amax/448, code = RNE-saturate(x * (448/amax)); amax == 0 gives

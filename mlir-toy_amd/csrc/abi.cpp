@@ -213,20 +213,30 @@ neptune_status neptune_decode_workspace_bytes(const neptune_decode_desc *d, size
 }
 
 namespace {
-// shared tail of the two decode entry points (pk != nullptr: paged KV)
+// shared tail of the decode entry points (pk != nullptr: paged KV;
+// workspace == kStaticScratch: the library's static device scratch)
+void *const kStaticScratch = reinterpret_cast<void *>(~uintptr_t(0));
+
 neptune_status decode_run(const neptune_decode_desc *d, const neptune_paged_kv_desc *pk,
                           const void *q, const void *k, const void *v, const float *k_scale,
                           const float *v_scale, const int32_t *block_table,
                           const int32_t *seq_lens, void *o, float *lse, void *workspace,
                           size_t workspace_bytes, void *stream) {
   if (!workspace) return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode: workspace is NULL");
+  const bool scratch = workspace == kStaticScratch;
   int64_t splits, chunk;
   decode_layout(d, &splits, &chunk);
   const size_t need = decode_ws_bytes(d, splits);
-  if (workspace_bytes < need)
+  if (scratch && need > kDecodeScratchBytes)
+    return fail(NEPTUNE_ERR_WORKSPACE_TOO_SMALL,
+                "decode_noalloc: %lld splits x %lld rows need %zu bytes of partials, the static "
+                "scratch holds %zu (use neptune_decode_splitk with a workspace)",
+                (long long)splits, (long long)(d->batch * d->heads_q), need,
+                kDecodeScratchBytes);
+  if (!scratch && workspace_bytes < need)
     return fail(NEPTUNE_ERR_WORKSPACE_TOO_SMALL, "decode: workspace %zu bytes, need %zu",
                 workspace_bytes, need);
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(workspace))
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || (!scratch && !aligned16(workspace)))
     return fail(NEPTUNE_ERR_UNSUPPORTED, "decode: q, k, v and workspace must be 16-byte aligned");
   DecodeLaunch L;
   L.q = q; L.k = k; L.v = v; L.k_scale = k_scale; L.v_scale = v_scale;
@@ -251,13 +261,17 @@ neptune_status decode_run(const neptune_decode_desc *d, const neptune_paged_kv_d
       L.v_pstride[i] = pk->v_stride[i];
     }
   }
-  const size_t rows = (size_t)d->batch * d->heads_q * splits;
-  L.part_o = (float *)workspace;
-  L.part_ml = (float *)((char *)workspace + align256(rows * d->head_dim * 4));
   const char *why = "";
   if (!decode_supported(L, &why)) return fail(NEPTUNE_ERR_UNSUPPORTED, "decode: %s", why);
   neptune_status st = device_ready();
   if (st != NEPTUNE_OK) return st;
+  if (scratch) {
+    st = hip_result(decode_scratch(&workspace), "decode_noalloc: scratch address");
+    if (st != NEPTUNE_OK) return st;
+  }
+  const size_t rows = (size_t)d->batch * d->heads_q * splits;
+  L.part_o = (float *)workspace;
+  L.part_ml = (float *)((char *)workspace + align256(rows * d->head_dim * 4));
   return hip_result(launch_decode(L, (hipStream_t)stream), "decode launch");
 }
 }  // namespace
@@ -275,6 +289,20 @@ neptune_status neptune_decode_splitk(const neptune_decode_desc *d, const void *q
     return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode: fp8 KV needs k_scale and v_scale");
   return decode_run(d, nullptr, q, k, v, k_scale, v_scale, nullptr, nullptr, o, lse, workspace,
                     workspace_bytes, stream);
+}
+
+neptune_status neptune_decode_splitk_noalloc(const neptune_decode_desc *d, const void *q,
+                                             const void *k, const void *v,
+                                             const float *k_scale, const float *v_scale,
+                                             void *o, float *lse, void *stream) {
+  neptune_status st = decode_check(d);
+  if (st != NEPTUNE_OK) return st;
+  if (!q || !k || !v || !o)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode_noalloc: q, k, v and o must be non-NULL");
+  if (d->kv_dtype == NEPTUNE_DTYPE_FP8_E4M3 && (!k_scale || !v_scale))
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode_noalloc: fp8 KV needs k_scale and v_scale");
+  return decode_run(d, nullptr, q, k, v, k_scale, v_scale, nullptr, nullptr, o, lse,
+                    kStaticScratch, 0, stream);
 }
 
 namespace {

@@ -22,6 +22,8 @@
 //                              transpose reads, B = P^T from S^T)
 // K/V loads are non-temporal: each byte is used once, and the nt hint
 // measured ~10% more HBM bandwidth for this stream.
+#include <mutex>
+
 #include "device_common.h"
 #include "kernels.h"
 #include "lds_dma.h"
@@ -908,6 +910,35 @@ hipError_t launch_decode(const DecodeLaunch &L, hipStream_t s) {
                      (const float *)L.part_o, (const float *)L.part_ml, (uint16_t *)L.o,
                      L.lse, (int32_t)L.splits);
   return hipGetLastError();
+}
+
+}  // namespace neptune
+
+// The split partials of neptune_decode_splitk_noalloc. Every GPU the library
+// runs on holds its own copy until the process ends. In host code the name
+// is only a stand-in: kernels receive the device address decode_scratch
+// resolves, never the array itself.
+static __device__ __align__(256) unsigned char scratch[neptune::kDecodeScratchBytes];
+
+namespace neptune {
+
+hipError_t decode_scratch(void **ptr) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void *addr[kMaxDevices] = {};
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    addr[dev] = p;
+  }
+  *ptr = addr[dev];
+  return hipSuccess;
 }
 
 hipError_t launch_kv_quantize(const QuantLaunch &q, hipStream_t s) {

@@ -53,6 +53,14 @@ struct ScanLaunch {
   int32_t delta_softplus;
 };
 
+// Bytes of the static device scratch behind neptune_decode_splitk_noalloc
+// (the split partials of one call: 520 bytes per (batch, query head, split)).
+constexpr size_t kDecodeScratchBytes = size_t(16) << 20;
+
+// Device address of that scratch on the current device, resolved once per
+// device by hipGetSymbolAddress and kept; hipSuccess or the HIP error.
+hipError_t decode_scratch(void **ptr);
+
 // Each returns hipSuccess or the launch error. Shapes the kernels do not
 // cover are rejected by the ABI layer before these are called.
 hipError_t launch_attn_fwd(const AttnLaunch &a, hipStream_t s);

@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "neptune_attn_fwd",
     "neptune_decode_workspace_bytes",
     "neptune_decode_splitk",
+    "neptune_decode_splitk_noalloc",
     "neptune_decode_paged",
     "neptune_decode_paged_fp8",
     "neptune_kv_quantize_fp8",
@@ -194,6 +195,10 @@ def _declare(lib: ctypes.CDLL) -> None:
         ctypes.POINTER(DecodeDesc), vp, vp, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp,
     ]
     lib.neptune_decode_splitk.restype = i32
+    lib.neptune_decode_splitk_noalloc.argtypes = [
+        ctypes.POINTER(DecodeDesc), vp, vp, vp, vp, vp, vp, vp, vp,
+    ]
+    lib.neptune_decode_splitk_noalloc.restype = i32
     lib.neptune_decode_paged.argtypes = [
         ctypes.POINTER(DecodeDesc), ctypes.POINTER(PagedKvDesc), vp, vp, vp, vp, vp, vp, vp, vp,
         ctypes.c_size_t, vp,
