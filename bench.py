@@ -6,7 +6,9 @@ configs[1]): causal bf16 prefill flash-attention B=4 H=32 S=4096 D=128 with
 per-row logsumexp, inputs ~ 0.5 N(0,1) resident in HBM. A step is one
 neptune_attn_fwd launch over that batch. The JSON line also carries, under
 "secondary", the split-K GQA decode (bf16 and fp8 KV, contiguous and paged)
-and selective-scan configurations measured the same way (GB/s against HBM).
+and selective-scan configurations measured the same way (GB/s against HBM),
+and config 1 (fp32 single-head attention, latency-bound, TFLOP/s), each with
+its own cpu_baseline.
 
 Each workload first runs untimed for SPINUP_S seconds (so the GPU is at its
 working clocks), then W warmup steps, then exactly K timed steps.
@@ -19,11 +21,12 @@ from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
 import sys
 import time
 from pathlib import Path
+
+import numpy as np
 
 ROOT = Path(__file__).resolve().parent
 for p in (ROOT, ROOT / "mlir-toy_amd"):
@@ -33,6 +36,7 @@ for p in (ROOT, ROOT / "mlir-toy_amd"):
 METRIC = "attention TFLOP/s (% MFMA peak); decode/scan GB/s (% HBM peak), 1 GPU"
 PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/clk/CU
 PEAK_HBM_GBS = 8000.0       # HBM3E
+PEAK_FP32_TFLOPS = 157.3    # dense fp32 MFMA
 
 
 def prefill_flops(B, H, S, D):
@@ -42,6 +46,39 @@ def prefill_flops(B, H, S, D):
 
 
 SPINUP_S = 1.0  # untimed run of each workload before its warmup steps
+CPU_BUDGET_S = 3.0  # CPU oracle seconds per secondary workload
+
+
+def _host_bits(t):
+    """A device tensor's storage as the numpy type the oracle takes."""
+    import numpy as np
+    import torch
+
+    t = t.detach().contiguous().cpu()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def _timed(fn):
+    t0 = time.perf_counter()
+    fn()
+    return time.perf_counter() - t0
+
+
+def _cpu_sample(run, units, per_unit, unit, scale, budget_s, what):
+    """cpu_baseline from run(i) -> seconds over units 0, 1, ... until
+    budget_s of CPU time or all units are spent; per_unit is the
+    algorithmic work (bytes or FLOPs) of one unit."""
+    import oracle
+
+    done, elapsed = 0, 0.0
+    while elapsed < budget_s and done < units:
+        elapsed += run(done)
+        done += 1
+    return {"value": per_unit * done / elapsed / scale, "unit": unit,
+            "cores": oracle.num_threads(), "kind": "port",
+            "sample": f"{done} {what} ({elapsed:.1f} s of CPU oracle time)"}
 
 
 def spin_up(fn, seconds, rotate=1):
@@ -123,7 +160,26 @@ def bench_decode(ops, torch, steps, warmup, fp8):
     scale_bytes = 2 * B * Hk * (L // 64) * 4 if fp8 else 0
     nbytes = kv_bytes + scale_bytes + 2 * B * Hq * D * 2
     name = "config5 fp8-KV split-K GQA decode" if fp8 else "config3 bf16 split-K GQA decode"
-    return name, wall, ev, nbytes
+
+    def cpu(budget_s):
+        """The oracle on whole batch rows of the same inputs, in order."""
+        import oracle
+
+        kvt = oracle.FP8 if fp8 else oracle.BF16
+        per_row = nbytes / B
+
+        def run(b):
+            sl = slice(b, b + 1)
+            args = [_host_bits(t[sl]) for t in (q, k, v)]
+            sc = [_host_bits(t[sl]) for t in (ks, vs)] if fp8 else [None, None]
+            t0 = time.perf_counter()
+            oracle.decode_splitk(*args, kvt, *sc, num_splits=splits)
+            return time.perf_counter() - t0
+
+        return _cpu_sample(run, B, per_row, "GB/s", 1e9, budget_s,
+                           "batch rows of the same decode")
+
+    return name, wall, ev, nbytes, cpu
 
 
 def bench_decode_paged(ops, torch, steps, warmup, page_size=64, fp8=False):
@@ -167,9 +223,31 @@ def bench_decode_paged(ops, torch, steps, warmup, page_size=64, fp8=False):
     nbytes = 2 * B * Hk * L * D * esize + B * per * 4 + 2 * B * Hq * D * 2
     if fp8:
         nbytes += 2 * B * per * Hk * 4  # the scales of every page read
+
+    def cpu(budget_s):
+        """The oracle's paged decode on one sequence at a time: that
+        sequence's pages (as the table orders them) form the pool it reads."""
+        import oracle
+
+        def run(b):
+            pages = table[b].long()
+            kq, vq = (_host_bits(pool.index_select(0, pages)) for pool in (k_pool, v_pool))
+            if not fp8:  # token-major storage, read through [pages, Hk, page, D] views
+                kq, vq = kq.transpose(0, 2, 1, 3), vq.transpose(0, 2, 1, 3)
+            sc = {n: _host_bits(t.index_select(0, pages)) for n, t in scales.items()}
+            tab = np.arange(per, dtype=np.int32)[None, :]
+            t0 = time.perf_counter()
+            oracle.decode_paged(_host_bits(q[b:b + 1]), kq, vq, tab, np.array([L], np.int32),
+                                max_seq_len=L, num_splits=splits, **sc)
+            return time.perf_counter() - t0
+
+        return _cpu_sample(run, B, nbytes / B, "GB/s", 1e9, budget_s,
+                           "sequences of the same paged decode")
+
+    if fp8:
         return ("config5 fp8-KV split-K GQA decode, paged KV (64-token head-major pages)", wall,
-                ev, nbytes)
-    return "config3 bf16 split-K GQA decode, paged KV (64-token pages)", wall, ev, nbytes
+                ev, nbytes, cpu)
+    return "config3 bf16 split-K GQA decode, paged KV (64-token pages)", wall, ev, nbytes, cpu
 
 
 def bench_scan(ops, torch, steps, warmup, rotate=2):
@@ -192,7 +270,65 @@ def bench_scan(ops, torch, steps, warmup, rotate=2):
 
     wall, ev = time_launches(step, steps, warmup, rotate)
     nbytes = 4 * Bn * Dm * L * 2 + 2 * Bn * N * L * 2 + Dm * N * 4 + 2 * Dm * 4
-    return "config4 Mamba-1 selective scan", wall, ev, nbytes
+
+    def cpu(budget_s, chunk=256):
+        """The oracle (fp64 recurrence) on 256-channel blocks of the first
+        input set, in order; bytes counted per channel (8 B per step, plus
+        its A, D and bias)."""
+        import oracle
+
+        u, dr, A, Bm, Cm, Dv, z, bias = sets[0]
+        Bh, Ch = _host_bits(Bm), _host_bits(Cm)
+        per_chunk = chunk * (L * 8 + N * 4 + 8)
+
+        def run(i):
+            b, c0 = divmod(i * chunk, Dm)
+            ch = slice(c0, c0 + chunk)
+            args = [_host_bits(t[b:b + 1, ch]) for t in (u, dr)]
+            t0 = time.perf_counter()
+            oracle.selective_scan(*args, _host_bits(A[ch]), Bh[b:b + 1], Ch[b:b + 1],
+                                  _host_bits(Dv[ch]), _host_bits(z[b:b + 1, ch]),
+                                  _host_bits(bias[ch]))
+            return time.perf_counter() - t0
+
+        return _cpu_sample(run, Bn * Dm // chunk, per_chunk, "GB/s", 1e9, budget_s,
+                           "256-channel blocks of the same scan")
+
+    return "config4 Mamba-1 selective scan", wall, ev, nbytes, cpu
+
+
+def bench_config1(ops, torch, steps, warmup, per_graph=100):
+    """Config 1: single-head fp32 attention B=1 H=1 S=128 D=64, non-causal,
+    the reference's CPU-runnable case. One launch is a few microseconds, far
+    less than the host's per-call cost, so a step replays a HIP graph of
+    `per_graph` captured launches and the figures are per launch."""
+    S, D = 128, 64
+    g = torch.Generator(device="cuda").manual_seed(1)
+    q, k, v = (torch.randn((1, 1, S, D), device="cuda", generator=g) for _ in range(3))
+    out = torch.empty_like(q)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # the first call loads the library off the capture
+        ops.attention(q, k, v, out=out)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(per_graph):
+            ops.attention(q, k, v, out=out)
+
+    wall, ev = time_launches(lambda _: graph.replay(), steps, warmup)
+    wall, ev = wall / per_graph, ev / per_graph
+    flops = 4.0 * S * S * D
+
+    def cpu(budget_s):
+        import oracle
+
+        qh, kh, vh = (_host_bits(t) for t in (q, k, v))
+        return _cpu_sample(lambda _: _timed(lambda: oracle.attn_fwd(qh, kh, vh, oracle.F32)),
+                           10**9, flops, "TFLOP/s", 1e12, budget_s,
+                           "repeated runs of the same config-1 attention")
+
+    return "config1 fp32 attention B1 H1 S128 D64 (latency-bound)", wall, ev, flops, cpu
 
 
 def cpu_baseline_prefill(res, budget_s=15.0, max_slices=64):
@@ -250,10 +386,10 @@ def bench_copy(torch, steps, warmup, nbytes=1 << 30):
     src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device="cuda").fill_(1.0)
     dst = torch.empty_like(src)
     wall, ev = time_launches(lambda _: dst.copy_(src), steps, warmup)
-    return "copy 1 GiB", wall, ev, 2 * nbytes
+    return "copy 1 GiB", wall, ev, 2 * nbytes, None
 
 
-def hbm_entry(key, name, wall, ev, nbytes, steps, traffic):
+def hbm_entry(key, name, wall, ev, nbytes, steps, traffic, cpu=None):
     gbs = nbytes / ev / 1e9
     return {
         "workload": name,
@@ -263,7 +399,43 @@ def hbm_entry(key, name, wall, ev, nbytes, steps, traffic):
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
                      "traffic": traffic.get(key)},
+        "cpu_baseline": cpu,
     }
+
+
+def config1_entry(name, wall, ev, flops, steps, cpu=None):
+    tf = flops / ev / 1e12
+    return {
+        "workload": name,
+        "value": round(flops * steps / wall / 1e12, 4),
+        "unit": "TFLOP/s",
+        "us_per_step": round(ev * 1e6, 2),
+        "roofline": {"bound": "mfma", "achieved": round(tf, 4), "peak": PEAK_FP32_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tf / PEAK_FP32_TFLOPS, 6),
+                     "traffic": None},
+        "cpu_baseline": cpu,
+    }
+
+
+def trace_summary(path, last):
+    """Markdown table of a rocprofv3 kernel-trace CSV: per kernel, every
+    launch, and the last `last` launches alone (the timed steps of a
+    single-workload run, after its spin-up and warmup launches)."""
+    import csv
+
+    runs = {}
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            t0, t1 = int(row["Start_Timestamp"]), int(row["End_Timestamp"])
+            runs.setdefault(row["Kernel_Name"], []).append((t0, t1 - t0))
+    print(f"| kernel | launches | avg µs (all) | last {last}: avg µs | min µs | max µs |")
+    print("|---|---|---|---|---|---|")
+    for name, rs in sorted(runs.items(), key=lambda kv: -sum(d for _, d in kv[1])):
+        rs.sort()
+        tail = [d / 1e3 for _, d in rs[-last:]]
+        allv = sum(d for _, d in rs) / len(rs) / 1e3
+        print(f"| `{name[:60]}` | {len(rs)} | {allv:.1f} | {sum(tail) / len(tail):.1f} | "
+              f"{min(tail):.1f} | {max(tail):.1f} |")
 
 
 def main():
@@ -276,14 +448,21 @@ def main():
                     help="skip the decode/scan configurations")
     ap.add_argument("--workload", default="all",
                     choices=["all", "prefill", "decode", "decode_fp8", "decode_paged",
-                             "decode_paged_fp8", "scan", "copy"],
+                             "decode_paged_fp8", "scan", "config1", "copy"],
                     help="run one configuration only (for profiling); 'copy' is a plain "
                          "1 GiB device copy used to calibrate HBM byte counters")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--spinup", type=float, default=SPINUP_S,
                     help="untimed seconds of each workload before its warmup steps "
                          "(0 for counter-collection runs, which need no steady clocks)")
+    ap.add_argument("--trace-summary", metavar="CSV",
+                    help="summarise a rocprofv3 kernel-trace CSV (no GPU work) and exit")
+    ap.add_argument("--last", type=int, default=20,
+                    help="with --trace-summary: launches per kernel counted as timed steps")
     args = ap.parse_args()
+    if args.trace_summary:
+        trace_summary(args.trace_summary, args.last)
+        return
     SPINUP_S = args.spinup
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -310,11 +489,15 @@ def main():
                                                        fp8=True),
         "scan": lambda: bench_scan(ops, torch, args.steps, args.warmup),
         "copy": lambda: bench_copy(torch, args.steps, args.warmup),
+        "config1": lambda: bench_config1(ops, torch, args.steps, args.warmup),
     }
     if args.workload in single:
-        name, wall, ev, nbytes = single[args.workload]()
-        print(json.dumps(hbm_entry(args.workload, name, wall, ev, nbytes, args.steps, traffic)),
-              flush=True)
+        name, wall, ev, work, cpu = single[args.workload]()
+        make = config1_entry if args.workload == "config1" else \
+            lambda *a, **kw: hbm_entry(args.workload, *a, **kw)
+        entry = make(name, wall, ev, work, args.steps, **({} if args.workload == "config1"
+                                                          else {"traffic": traffic}))
+        print(json.dumps(entry), flush=True)
         return
 
     res = bench_prefill(ops, torch, args.steps, args.warmup)
@@ -335,11 +518,18 @@ def main():
                                                                     sec_warm)),
                         ("decode_paged_fp8", lambda: bench_decode_paged(ops, torch, sec_steps,
                                                                         sec_warm, fp8=True)),
-                        ("scan", lambda: bench_scan(ops, torch, sec_steps, sec_warm))):
-            name, wall, ev, nbytes = fn()
-            secondary.append(hbm_entry(key, name, wall, ev, nbytes, sec_steps, traffic))
-            print(f"# {name}: {ev * 1e6:.1f} us, {nbytes / ev / 1e9:.0f} GB/s", file=sys.stderr,
-                  flush=True)
+                        ("scan", lambda: bench_scan(ops, torch, sec_steps, sec_warm)),
+                        ("config1", lambda: bench_config1(ops, torch, sec_steps, sec_warm))):
+            name, wall, ev, work, cpu_fn = fn()
+            cpu = None if args.no_cpu else cpu_fn(CPU_BUDGET_S)
+            if key == "config1":  # wall and ev are per launch: steps x launches per graph
+                secondary.append(config1_entry(name, wall, ev, work, sec_steps, cpu))
+                print(f"# {name}: {ev * 1e6:.1f} us, {work / ev / 1e12:.3f} TFLOP/s",
+                      file=sys.stderr, flush=True)
+            else:
+                secondary.append(hbm_entry(key, name, wall, ev, work, sec_steps, traffic, cpu))
+                print(f"# {name}: {ev * 1e6:.1f} us, {work / ev / 1e9:.0f} GB/s",
+                      file=sys.stderr, flush=True)
             torch.cuda.empty_cache()
         # the prefill inputs are needed again for the CPU sample
         g = torch.Generator(device="cuda").manual_seed(2)

@@ -14,13 +14,16 @@ other field by field.
 from __future__ import annotations
 
 import ctypes
+import os
 import subprocess
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB_PATH = HERE / "libneptune_oracle.so"
+# NEPTUNE_ORACLE_LIB selects another build of the same source (the
+# host-sanitizer build of oracle/Makefile's `sanitize` target)
+LIB_PATH = Path(os.environ.get("NEPTUNE_ORACLE_LIB") or HERE / "libneptune_oracle.so")
 
 F32, F16, BF16, FP8 = 0, 1, 2, 3
 _NP_STORAGE = {F32: np.float32, F16: np.float16, BF16: np.uint16, FP8: np.uint8}
