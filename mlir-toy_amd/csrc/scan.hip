@@ -35,6 +35,26 @@
 //          the four waves' sums meet in LDS.
 //   store  each thread adds the four wave sums for its two steps, applies
 //          D*u and the gate and stores two bf16 outputs.
+//
+// Sequence-parallel path. When batch * dim / 16 work-groups cannot fill the
+// GPU (few channels, long sequences), the sequence is cut into nch chunks of
+// T steps (the last one takes the remainder, T .. 2T - 1 steps) and the
+// scan runs in three launches, using y itself as scratch (no workspace):
+//   state   every chunk but the last scans from x = 0 without outputs and
+//           leaves its end state x_end[16] and its delta sum S (fp32) at the
+//           start of its own y segment (T >= 64 steps: 128 bytes >= 68);
+//   carry   one lane per (batch, channel, state) walks the chunks in order,
+//           x_start[k + 1] = 2^(A S[k] log2 e) x_start[k] + x_end[k] (the
+//           decay over a chunk is the product of its steps' decays), and
+//           leaves x_start[k] where x_end[k] was;
+//   output  every chunk reads its x_start from its own segment, then scans
+//           it with outputs, overwriting the segment.
+// Each launch touches only its own chunk's segment, so work-groups never
+// race on the scratch. The work is about 1.6 times the single pass's (the
+// state pass repeats the updates without outputs), which pays once the
+// chunks multiply the work-groups enough to fill the GPU.
+#include <algorithm>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -53,7 +73,17 @@ struct ScanArgs {
   uint16_t *y;
   int32_t Dm, L, softplus;
   int32_t vec;  // 4-byte pair access: L even and every base 4-byte aligned
+  int32_t T, nch;  // chunk length and count (1 chunk of L: the single pass)
 };
+
+// the single pass, and the state and output passes of the chunked path
+enum ScanMode { kScanFull = 0, kScanState = 1, kScanOutput = 2 };
+
+// chunk k of channel d of batch row b: its y segment as fp32 scratch
+// (x[16], then S)
+__device__ inline float *chunk_scratch(const ScanArgs &a, int b, int d, int k) {
+  return reinterpret_cast<float *>(a.y + ((int64_t)b * a.Dm + d) * a.L + (int64_t)k * a.T);
+}
 
 __device__ inline float lo_bf16(uint32_t p) { return __uint_as_float(p << 16); }
 __device__ inline float hi_bf16(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
@@ -90,6 +120,7 @@ __device__ inline float fold16(float a, float b) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+template <int MODE>
 __global__ __launch_bounds__(NT) void selective_scan_fwd(ScanArgs a) {
   // (delta, delta*u) and (B, C) for two steps per float4; one float4 of
   // padding per row keeps the 16 rows read together in distinct banks
@@ -101,15 +132,25 @@ __global__ __launch_bounds__(NT) void selective_scan_fwd(ScanArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = tid >> 6;
   const int nblk = (a.Dm + SCH - 1) / SCH;
-  const int b = blockIdx.x / nblk;
-  const int d0 = (blockIdx.x % nblk) * SCH;
+  // work-group -> (batch row, channel block, chunk); the state pass has no
+  // work-group for the last chunk, whose end state nothing reads
+  const int nwch = MODE == kScanState ? a.nch - 1 : a.nch;
+  const int kc = (int)(blockIdx.x % (unsigned)nwch);
+  const int grp = (int)(blockIdx.x / (unsigned)nwch);
+  const int b = grp / nblk;
+  const int d0 = (grp % nblk) * SCH;
+  const int tb = kc * a.T;
+  const int te = kc == a.nch - 1 ? a.L : tb + a.T;
 
   // scan identity: channel c, state n
   const int c = lane & 15, r = lane >> 4;
   const int n = 4 * w + r;
   const bool cok = d0 + c < a.Dm;
   const float A2 = cok ? a.A[(int64_t)(d0 + c) * ST + n] * kLog2e : 0.0f;
-  float x = 0.0f;
+  // the output pass starts from the carried state the carry pass left in
+  // this chunk's segment (read here, before any store overwrites it)
+  float x = (MODE == kScanOutput && cok) ? chunk_scratch(a, b, d0 + c, kc)[n] : 0.0f;
+  float dsum = 0.0f;  // state pass: this thread's share of the chunk's delta sum
 
   // stage / store identity: channel sc, steps 2 sp and 2 sp + 1 of a chunk;
   // B / C identity: state tid / 16, same step pair
@@ -134,23 +175,23 @@ __global__ __launch_bounds__(NT) void selective_scan_fwd(ScanArgs a) {
       if (sok) {
         pu = *(const uint32_t *)(a.u + srow + t);
         pdr = *(const uint32_t *)(a.dr + srow + t);
-        if (a.z) pz = *(const uint32_t *)(a.z + srow + t);
+        if (MODE != kScanState && a.z) pz = *(const uint32_t *)(a.z + srow + t);
       }
       pB = *(const uint32_t *)(a.Bm + bcrow + t);
-      pC = *(const uint32_t *)(a.Cm + bcrow + t);
+      if (MODE != kScanState) pC = *(const uint32_t *)(a.Cm + bcrow + t);
     } else {
       if (sok) {
         pu = load_pair(a.u + srow, t, a.L, vec);
         pdr = load_pair(a.dr + srow, t, a.L, vec);
-        pz = a.z ? load_pair(a.z + srow, t, a.L, vec) : 0u;
+        pz = (MODE != kScanState && a.z) ? load_pair(a.z + srow, t, a.L, vec) : 0u;
       }
       pB = load_pair(a.Bm + bcrow, t, a.L, vec);
-      pC = load_pair(a.Cm + bcrow, t, a.L, vec);
+      if (MODE != kScanState) pC = load_pair(a.Cm + bcrow, t, a.L, vec);
     }
   };
 
-  fetch(0);
-  for (int t0 = 0; t0 < a.L; t0 += TT) {
+  fetch(tb);
+  for (int t0 = tb; t0 < te; t0 += TT) {
     // ---- stage
     float du2[2], gate[2];
     {
@@ -167,14 +208,33 @@ __global__ __launch_bounds__(NT) void selective_scan_fwd(ScanArgs a) {
         const float delta = in ? (a.softplus ? softplus_fast(v) : v) : 0.0f;
         pf[2 * i] = delta;
         pf[2 * i + 1] = delta * uu[i];
-        du2[i] = Dd * uu[i];
-        gate[i] = a.z ? silu_fast(zz[i]) : 1.0f;
+        if constexpr (MODE == kScanState) {
+          dsum += delta;
+        } else {
+          du2[i] = Dd * uu[i];
+          gate[i] = a.z ? silu_fast(zz[i]) : 1.0f;
+        }
       }
       pre[sc][sp] = pv;
       bcs[bn][sp] = make_float4(lo_bf16(pB), lo_bf16(pC), hi_bf16(pB), hi_bf16(pC));
     }
-    if (t0 + TT < a.L) fetch(t0 + TT);
+    if (t0 + TT < te) fetch(t0 + TT);
     __syncthreads();
+
+    if constexpr (MODE == kScanState) {
+      // the recurrence alone
+#pragma unroll
+      for (int j = 0; j < TP; ++j) {
+        const float4 pd = pre[c][j];
+        const float4 q = bcs[n][j];
+        x = fmaf(fast_exp2(pd.x * A2), x, pd.y * q.x);
+        x = fmaf(fast_exp2(pd.z * A2), x, pd.w * q.z);
+      }
+      // pre / bcs are rewritten by the next stage only after every wave is
+      // done with them
+      __syncthreads();
+      continue;
+    }
 
     // ---- scan: C_n x_n per step
     float p[TT];
@@ -221,9 +281,69 @@ __global__ __launch_bounds__(NT) void selective_scan_fwd(ScanArgs a) {
     // passed this chunk's second barrier, and part only after the next
     // chunk's first barrier, which every wave reaches after its stores
   }
+  if constexpr (MODE == kScanState) {
+    // the chunk's end state and delta sum, at the start of its own segment
+    if (cok) chunk_scratch(a, b, d0 + c, kc)[n] = x;
+#pragma unroll
+    for (int off = 1; off < TP; off <<= 1) dsum += __shfl_xor(dsum, off, 64);
+    if (sok && sp == 0) chunk_scratch(a, b, sd, kc)[ST] = dsum;
+  }
+}
+
+// The carry pass: one lane per (batch row, channel, state) walks the chunks
+// in order and leaves each chunk's starting state where its end state was.
+__global__ __launch_bounds__(256) void selective_scan_carry(ScanArgs a, int32_t lanes) {
+  const int gid = blockIdx.x * 256 + threadIdx.x;
+  if (gid >= lanes) return;
+  const int n = gid & (ST - 1), bd = gid / ST;
+  const int b = bd / a.Dm, d = bd - b * a.Dm;
+  const float A2 = a.A[(int64_t)d * ST + n] * kLog2e;
+  float carry = 0.0f;
+  float *p = chunk_scratch(a, b, d, 0);
+  float xe = p[n], S = p[ST];
+  for (int k = 0; k + 1 < a.nch; ++k) {
+    // the next chunk's summary is read before this chunk's is overwritten
+    float *pn = chunk_scratch(a, b, d, k + 1);
+    float xe_n = 0.0f, S_n = 0.0f;
+    if (k + 2 < a.nch) {
+      xe_n = pn[n];
+      S_n = pn[ST];
+    }
+    p[n] = carry;
+    carry = fmaf(fast_exp2(A2 * S), carry, xe);
+    p = pn;
+    xe = xe_n;
+    S = S_n;
+  }
+  p[n] = carry;  // the last chunk's starting state
 }
 
 }  // namespace
+
+// Chunking of the sequence-parallel path: used when the single pass would
+// launch fewer than kScanFillGroups work-groups (four per CU) and the
+// sequence holds at least two 64-step chunks; the chunk count brings the
+// launch to about kScanTargetGroups work-groups (five per CU, what the
+// single pass gets at config 4). T is a multiple of 32 steps and at least
+// 64; the last chunk takes the remainder (T .. 2T - 1 steps). nch = 1: the
+// single pass. The chunked path needs the 4-byte pair access (even L).
+constexpr int64_t kScanFillGroups = 1024, kScanTargetGroups = 1280, kScanMinChunk = 64;
+
+void scan_chunking(int64_t batch, int64_t dim, int64_t L, bool vec, int32_t *T, int32_t *nch) {
+  const int64_t groups = (dim + SCH - 1) / SCH * batch;
+  *T = (int32_t)L;
+  *nch = 1;
+  if (!vec || groups >= kScanFillGroups || L < 2 * kScanMinChunk) return;
+  int64_t want = (kScanTargetGroups + groups - 1) / groups;
+  want = std::min(want, L / kScanMinChunk);
+  if (want < 2) return;
+  int64_t t = (L + want - 1) / want;
+  t = std::max<int64_t>((t + TT - 1) / TT * TT, kScanMinChunk);
+  const int64_t k = L / t;  // the last chunk absorbs the remainder
+  if (k < 2) return;
+  *T = (int32_t)t;
+  *nch = (int32_t)k;
+}
 
 bool scan_supported(const ScanLaunch &a, const char **why) {
   if (a.d_state != ST) {
@@ -255,8 +375,19 @@ hipError_t launch_selective_scan(const ScanLaunch &L, hipStream_t s) {
   auto al4 = [](const void *p) { return ((uintptr_t)p & 3u) == 0; };
   a.vec = (L.seq_len % 2 == 0) && al4(L.u) && al4(L.delta_raw) && al4(L.B) && al4(L.C) &&
           al4(L.y) && (!L.z || al4(L.z));
-  const int64_t nblk = (L.dim + SCH - 1) / SCH;
-  hipLaunchKernelGGL(selective_scan_fwd, dim3((unsigned)(nblk * L.batch)), dim3(NT), 0, s, a);
+  const int64_t groups = (L.dim + SCH - 1) / SCH * L.batch;
+  scan_chunking(L.batch, L.dim, L.seq_len, a.vec != 0, &a.T, &a.nch);
+  if (a.nch <= 1) {
+    hipLaunchKernelGGL(selective_scan_fwd<kScanFull>, dim3((unsigned)groups), dim3(NT), 0, s, a);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL(selective_scan_fwd<kScanState>, dim3((unsigned)(groups * (a.nch - 1))),
+                     dim3(NT), 0, s, a);
+  const int64_t lanes = L.batch * L.dim * ST;
+  hipLaunchKernelGGL(selective_scan_carry, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0,
+                     s, a, (int32_t)lanes);
+  hipLaunchKernelGGL(selective_scan_fwd<kScanOutput>, dim3((unsigned)(groups * a.nch)), dim3(NT),
+                     0, s, a);
   return hipGetLastError();
 }
 

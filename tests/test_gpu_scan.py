@@ -88,3 +88,60 @@ def test_config4_full_shape(ops):
     torch.cuda.synchronize()
     chan = torch.tensor([0, 1, 2, 777, 2048, 4095, 5000, 5119])
     _check(y.cpu(), ins, chan)
+
+
+def _chunked(b, d, L):
+    """Whether the library takes the sequence-parallel path for this shape
+    (the rule of scan_chunking in scan.hip: fewer than 1024 work-groups of 16
+    channels, an even length and at least two 64-step chunks)."""
+    groups = -(-d // 16) * b
+    return L % 2 == 0 and groups < 1024 and L >= 128
+
+
+@pytest.mark.parametrize("b,d,L,bias,gate", [
+    (1, 64, 65536, True, True),    # 4 channel blocks over a long sequence: 292 chunks
+    (1, 16, 4096, False, True),    # one channel block, 64 chunks of 64 steps
+    (2, 48, 1000, True, False),    # ragged channel block, last chunk longer than T
+    (1, 8, 130, True, True),       # two chunks, the second 66 steps
+])
+def test_scan_sequence_parallel_matches_oracle(ops, b, d, L, bias, gate):
+    """The chunked path (state pass, carry pass, output pass, with y as the
+    scratch of the chunk carries) against the fp64 sequential oracle."""
+    assert _chunked(b, d, L)
+    _log(f"case: scan chunked b={b} d={d} L={L} bias={bias} gate={gate}")
+    u, dr, A, Bm, Cm, D, z, bias_t = scan_inputs(b, d, L, seed=200 + L, with_bias=bias)
+    y = ops.selective_scan(u.cuda(), dr.cuda(), A.cuda(), Bm.cuda(), Cm.cuda(), D.cuda(),
+                           z.cuda() if gate else None,
+                           bias_t.cuda() if bias_t is not None else None)
+    torch.cuda.synchronize()
+    ref_bits, _ = oracle.selective_scan(bits(u), bits(dr), A.numpy(), bits(Bm), bits(Cm),
+                                        D.numpy(), bits(z) if gate else None,
+                                        None if bias_t is None else bias_t.numpy())
+    ref = oracle.decode(ref_bits, oracle.BF16).astype(np.float64)
+    got = to_f32(y).astype(np.float64)
+    assert np.isfinite(got).all()
+    bad = np.abs(got - ref) > 2e-2 * np.maximum(1.0, np.abs(ref))
+    assert not bad.any(), (np.argwhere(bad)[:5], np.abs(got - ref).max())
+
+
+@pytest.mark.parametrize("b,d,L", [(1, 32, 129), (4, 4096, 256), (2, 64, 126)])
+def test_scan_single_pass_matches_oracle(ops, b, d, L):
+    """Shapes the single pass keeps: an odd length, enough channel blocks to
+    fill the GPU, and a sequence too short for two chunks."""
+    assert not _chunked(b, d, L)
+    _log(f"case: scan single pass b={b} d={d} L={L}")
+    ins = scan_inputs(b, d, L, seed=300 + L)
+    y = ops.selective_scan(*(t.cuda() for t in ins))
+    torch.cuda.synchronize()
+    _check(y, ins)
+
+
+def test_scan_chunked_repeated_call_is_identical(ops):
+    """y serves as the chunked path's scratch: a second call into the same
+    buffer (holding the first call's outputs) gives bit-identical results."""
+    _log("case: scan chunked repeat")
+    ins = [t.cuda() for t in scan_inputs(1, 32, 2048, seed=9)]
+    y1 = ops.selective_scan(*ins)
+    y2 = ops.selective_scan(*ins)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
