@@ -37,6 +37,12 @@ METRIC = "attention TFLOP/s (% MFMA peak); decode/scan GB/s (% HBM peak), 1 GPU"
 PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/clk/CU
 PEAK_HBM_GBS = 8000.0       # HBM3E
 PEAK_FP32_TFLOPS = 157.3    # dense fp32 MFMA
+# Selective-scan VALU roofline: a state update is one v_exp_f32 (1.8 FMA
+# issue slots on gfx950, measured) plus two multiplies and two FMAs, 5.8
+# slots; a wave64 VALU op takes one 16-lane slot per SIMD per clock:
+# 256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz / 5.8 slots.
+SCAN_SLOTS_PER_UPDATE = 5.8
+PEAK_SCAN_TUPS = 256 * 4 * 16 * 2.4e9 / SCAN_SLOTS_PER_UPDATE / 1e12
 
 
 def prefill_flops(B, H, S, D):
@@ -297,6 +303,15 @@ def bench_scan(ops, torch, steps, warmup, rotate=2):
     return "config4 Mamba-1 selective scan", wall, ev, nbytes, cpu
 
 
+def scan_valu_roofline(ev, Bn=4, L=2048, Dm=5120, N=16):
+    """The scan against its vector-ALU bound (state updates per second)."""
+    tups = Bn * Dm * L * N / ev / 1e12
+    return {"bound": "valu", "achieved": round(tups, 3), "peak": round(PEAK_SCAN_TUPS, 3),
+            "unit": "T state-updates/s", "frac": round(tups / PEAK_SCAN_TUPS, 4),
+            "basis": f"{SCAN_SLOTS_PER_UPDATE} VALU issue slots per state update (v_exp_f32 "
+                     "1.8 + two mul + two fma), 16 lanes x 1024 SIMDs x 2.4 GHz"}
+
+
 def bench_config1(ops, torch, steps, warmup, per_graph=100):
     """Config 1: single-head fp32 attention B=1 H=1 S=128 D=64, non-causal,
     the reference's CPU-runnable case. One launch is a few microseconds, far
@@ -497,6 +512,8 @@ def main():
             lambda *a, **kw: hbm_entry(args.workload, *a, **kw)
         entry = make(name, wall, ev, work, args.steps, **({} if args.workload == "config1"
                                                           else {"traffic": traffic}))
+        if args.workload == "scan":
+            entry["roofline_valu"] = scan_valu_roofline(ev)
         print(json.dumps(entry), flush=True)
         return
 
@@ -528,6 +545,8 @@ def main():
                       file=sys.stderr, flush=True)
             else:
                 secondary.append(hbm_entry(key, name, wall, ev, work, sec_steps, traffic, cpu))
+                if key == "scan":
+                    secondary[-1]["roofline_valu"] = scan_valu_roofline(ev)
                 print(f"# {name}: {ev * 1e6:.1f} us, {work / ev / 1e9:.0f} GB/s",
                       file=sys.stderr, flush=True)
             torch.cuda.empty_cache()

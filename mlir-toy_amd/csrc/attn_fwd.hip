@@ -242,24 +242,34 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_mfma(AttnArgs a) {
   }
 }
 
-// fp32 path (config 1 and any F32 request): one wave per 64 query rows,
-// one lane per row, K/V blocks staged in LDS and read as broadcasts. The
-// recurrence is the HTile one with no rounding of P (the input type is
-// fp32).
-constexpr int F32_BM = 64;
+// fp32 path (config 1 and any F32 request): a 256-thread work-group per 16
+// query rows, 16 lanes per row. K/V blocks of 64 keys are staged in LDS;
+// lane k of a row takes keys k, k + 16, k + 32, k + 48 of each block and
+// keeps its own online-softmax state (m, l, acc) over them, the HTile
+// recurrence with no rounding of P (the input type is fp32). The 16 states
+// of a row are merged at the end in the exp2 domain, M = max m_k,
+// l = sum 2^(m_k - M) l_k, acc = sum 2^(m_k - M) acc_k (the flash-decoding
+// combine), so a short sequence still spreads over many waves.
+constexpr int F32_BM = 16;   // query rows per work-group
+constexpr int F32_KS = 16;   // lanes per row, each taking every 16th key
+constexpr int F32_NT = F32_BM * F32_KS;
 
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(64) void attn_fwd_f32(AttnArgs a) {
-  __shared__ float Ks[BN][D];
-  __shared__ float Vs[BN][D];
+__global__ __launch_bounds__(F32_NT) void attn_fwd_f32(AttnArgs a) {
+  // rows padded by 4 floats: the 16 lanes of a row read 16 different keys
+  // at one head_dim offset, spread over the banks
+  constexpr int DP = D + 4;
+  __shared__ __attribute__((aligned(16))) float Ks[BN][DP];
+  __shared__ __attribute__((aligned(16))) float Vs[BN][DP];
   const int t = threadIdx.x;
+  const int rl = t / F32_KS, kl = t % F32_KS;
   const int id = blockIdx.x;
   const int qb = id / a.BH, bh = id % a.BH;
   const int b = bh / a.Hq, h = bh % a.Hq, hk = h / a.group;
   const float *qp = (const float *)a.q + b * a.qs0 + h * a.qs1;
   const float *kp = (const float *)a.k + b * a.ks0 + hk * a.ks1;
   const float *vp = (const float *)a.v + b * a.vs0 + hk * a.vs1;
-  const int row = qb * F32_BM + t;
+  const int row = qb * F32_BM + rl;
 
   float q[D], acc[D];
 #pragma unroll
@@ -274,54 +284,73 @@ __global__ __launch_bounds__(64) void attn_fwd_f32(AttnArgs a) {
     int lim = last < 0 ? 0 : last / BN + 1;
     nkb = nkb < lim ? nkb : lim;
   }
+  constexpr int KPL = BN / F32_KS;  // keys per lane and block
   for (int jb = 0; jb < nkb; ++jb) {
     const int key0 = jb * BN;
     __syncthreads();
-    for (int e = t; e < BN * D; e += 64) {
-      int r = e / D, c = e % D, key = key0 + r;
+    for (int e = t; e < BN * D; e += F32_NT) {
+      const int r = e / D, c = e % D, key = key0 + r;
       Ks[r][c] = key < a.Sk ? kp[key * a.ks2 + c] : 0.0f;
       Vs[r][c] = key < a.Sk ? vp[key * a.vs2 + c] : 0.0f;
     }
     __syncthreads();
-    float s[BN];
+    float s[KPL];
     float mx = -INFINITY;
-#pragma unroll 4
-    for (int j = 0; j < BN; ++j) {
+#pragma unroll
+    for (int jj = 0; jj < KPL; ++jj) {
+      const int j = F32_KS * jj + kl;
       float dot = 0.0f;
 #pragma unroll
       for (int d = 0; d < D; ++d) dot = fmaf(q[d], Ks[j][d], dot);
-      int key = key0 + j;
+      const int key = key0 + j;
       float sv = dot * a.scale2;
       if (key >= a.Sk || (CAUSAL && key > row + a.off)) sv = -INFINITY;
-      s[j] = sv;
+      s[jj] = sv;
       mx = fmaxf(mx, sv);
     }
     const float m_new = fmaxf(m, mx);
     const float alpha = fast_exp2(m - m_new);
     float rs = 0.0f;
 #pragma unroll
-    for (int j = 0; j < BN; ++j) {
-      s[j] = fast_exp2(s[j] - m_new);
-      rs += s[j];
+    for (int jj = 0; jj < KPL; ++jj) {
+      s[jj] = fast_exp2(s[jj] - m_new);
+      rs += s[jj];
     }
     lsum = lsum * alpha + rs;
     m = m_new;
 #pragma unroll
     for (int d = 0; d < D; ++d) acc[d] *= alpha;
-#pragma unroll 4
-    for (int j = 0; j < BN; ++j) {
-      const float p = s[j];
 #pragma unroll
-      for (int d = 0; d < D; ++d) acc[d] = fmaf(p, Vs[j][d], acc[d]);
+    for (int jj = 0; jj < KPL; ++jj) {
+      const float pj = s[jj];
+      const int j = F32_KS * jj + kl;
+#pragma unroll
+      for (int d = 0; d < D; ++d) acc[d] = fmaf(pj, Vs[j][d], acc[d]);
     }
   }
-  if (row < a.Sq) {
+  // merge the 16 lane states of the row (lanes rl * 16 .. rl * 16 + 15 of
+  // one wave): a lane that saw no visible key has m = -FLT_MAX and l = 0
+  float M = m;
+#pragma unroll
+  for (int off = 1; off < F32_KS; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+  const float wgt = fast_exp2(m - M);
+  float ltot = lsum * wgt;
+#pragma unroll
+  for (int off = 1; off < F32_KS; off <<= 1) ltot += __shfl_xor(ltot, off, 64);
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    float v = acc[d] * wgt;
+#pragma unroll
+    for (int off = 1; off < F32_KS; off <<= 1) v += __shfl_xor(v, off, 64);
+    acc[d] = v;
+  }
+  if (row < a.Sq && kl == 0) {
     float *op = (float *)a.o + b * a.os0 + h * a.os1 + row * a.os2;
 #pragma unroll
-    for (int d = 0; d < D; ++d) op[d] = lsum > 0.0f ? acc[d] / lsum : 0.0f;
+    for (int d = 0; d < D; ++d) op[d] = ltot > 0.0f ? acc[d] / ltot : 0.0f;
     if (a.lse)
       a.lse[((int64_t)b * a.Hq + h) * a.Sq + row] =
-          lsum > 0.0f ? (m + log2f(lsum)) * kLn2 : -INFINITY;
+          ltot > 0.0f ? (M + log2f(ltot)) * kLn2 : -INFINITY;
   }
 }
 
@@ -336,9 +365,9 @@ void launch_mfma(const AttnArgs &args, bool causal, int grid, hipStream_t s) {
 template <int D>
 void launch_f32(const AttnArgs &args, bool causal, int grid, hipStream_t s) {
   if (causal)
-    hipLaunchKernelGGL((attn_fwd_f32<D, true>), dim3(grid), dim3(64), 0, s, args);
+    hipLaunchKernelGGL((attn_fwd_f32<D, true>), dim3(grid), dim3(F32_NT), 0, s, args);
   else
-    hipLaunchKernelGGL((attn_fwd_f32<D, false>), dim3(grid), dim3(64), 0, s, args);
+    hipLaunchKernelGGL((attn_fwd_f32<D, false>), dim3(grid), dim3(F32_NT), 0, s, args);
 }
 
 }  // namespace
@@ -385,8 +414,8 @@ bool attn_supported(const AttnLaunch &a, const char **why) {
   }
   // a dispatch covers at most 2^32 - 1 work-items: one 256-thread work-group
   // per 128 query rows and (batch, head) (the most any 16-bit path launches),
-  // one 64-thread work-group per 64 rows for fp32
-  const int64_t rows = a.dtype == 0 ? F32_BM : BM, thr = a.dtype == 0 ? 64 : NTHR;
+  // one 256-thread work-group per 16 rows for fp32
+  const int64_t rows = a.dtype == 0 ? F32_BM : BM, thr = a.dtype == 0 ? F32_NT : NTHR;
   if ((a.seq_q + rows - 1) / rows * (a.batch * a.heads_q) * thr > (int64_t)0xffffffff) {
     *why = "batch*heads*seq_q too large for one launch";
     return false;

@@ -52,6 +52,32 @@ def test_config1_fp32_matches_oracle(ops):
     assert max_abs(to_f32(lse), exact_lse) <= 1e-5 * np.abs(exact_lse).max()
 
 
+@pytest.mark.parametrize("B,Hq,Hk,Sq,Sk,D,causal", [
+    (2, 4, 2, 100, 100, 32, True),    # GQA, a partial 16-row block, causal
+    (1, 2, 1, 70, 300, 128, False),   # queries shorter than keys, ragged key block
+    (1, 2, 2, 33, 33, 64, True),      # a row block holding one valid row
+    (1, 1, 1, 200, 150, 64, True),    # more queries than keys: early rows see no key
+])
+def test_fp32_shapes_match_oracle(ops, B, Hq, Hk, Sq, Sk, D, causal):
+    """The fp32 path (16 lanes per query row, each over every 16th key, merged
+    at the end) at 1e-5 relative of the oracle, LSE included; rows with no
+    visible key give O = 0 and LSE = -inf."""
+    _log(f"case: fp32 B={B} Hq={Hq} Hk={Hk} Sq={Sq} Sk={Sk} D={D} causal={causal}")
+    q = randn((B, Hq, Sq, D), seed=11, dtype=torch.float32)
+    k = randn((B, Hk, Sk, D), seed=12, dtype=torch.float32)
+    v = randn((B, Hk, Sk, D), seed=13, dtype=torch.float32)
+    out, lse = ops.attention(q.cuda(), k.cuda(), v.cuda(), causal=causal, return_lse=True)
+    torch.cuda.synchronize()
+    ref_o, ref_lse = _oracle_attn(q, k, v, causal)
+    got = to_f32(out)
+    assert np.isfinite(got).all()
+    assert max_abs(got, ref_o) <= TOL_F32_REL * np.abs(ref_o).max()
+    got_lse = to_f32(lse)
+    assert np.array_equal(np.isneginf(got_lse), np.isneginf(ref_lse))
+    fin = np.isfinite(ref_lse)
+    assert max_abs(got_lse[fin], ref_lse[fin]) <= 1e-5 * np.abs(ref_lse[fin]).max()
+
+
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("head_dim", [128, 64])
