@@ -23,6 +23,7 @@
 // K/V loads are non-temporal: each byte is used once, and the nt hint
 // measured ~10% more HBM bandwidth for this stream.
 #include <mutex>
+#include <type_traits>
 
 #include "device_common.h"
 #include "kernels.h"
@@ -375,30 +376,69 @@ __global__ __launch_bounds__(RT) void decode_partial_ring(DecArgs a) {
   }
 }
 
-// fp8-E4M3 KV through LDS, the same ring design as decode_partial_ring with
-// 1-byte codes: K and V tiles of 32 tokens x 128 B (4 KiB) per slot, filled
-// by non-temporal global_load_lds_dwordx4. Codes are widened to bf16 in
+// fp8-E4M3 KV: K codes straight into registers, V codes through an LDS
+// ring. A 32-token step is 4 KiB of K and 4 KiB of V codes; R8P steps are
+// in flight. Each lane loads the 64 K codes it feeds to S^T = K.Q^T with
+// four non-temporal global_load_dwordx4 into a register buffer (one buffer
+// per step in flight), so only V -- which the MFMA needs transposed, by
+// ds_read_b64_tr_b8 -- takes LDS: the ring holds R8P V tiles (16 KiB per
+// wave) and the register file holds the K tiles, twice the bytes in flight
+// of a ring of K and V tiles in the same LDS. Codes are widened to bf16 in
 // registers (exact); the per-(token block) K scale folds into the score
 // scale and the V scale into P before its bf16 rounding. 32-token steps
 // never straddle a scale block (the block is a multiple of 32 and every
 // wave range starts on a 32-token boundary). PAGED: the pools are addressed
 // through the block table as in decode_partial_ring<true>, and the page is
 // the scale block (one K and one V scale per page and kv head).
-//   K tile: 16-byte unit u of row r at u ^ ((r >> 1) & 7); a lane reads the
-//           16 codes of head_dim 64 sp + 16 G .. +15 (two MFMA k-steps).
-//   V tile: same layout; V^T comes from ds_read_b64_tr_b8, whose source
-//           lane pair (2i, 2i+1) names the token row of k-slot i, so the
-//           rows can follow the P^T key order directly.
+//   K: lane (n, G) loads rows n and 16 + n of the step, head_dim
+//      64 sp + 16 G .. +15 (sp = 0, 1): the A operand of two MFMA k-steps.
+//   V tile: 16-byte unit u of row r at u ^ ((r >> 1) & 7); V^T comes from
+//      ds_read_b64_tr_b8, whose source lane pair (2i, 2i+1) names the token
+//      row of k-slot i, so the rows can follow the P^T key order directly.
+// The K loads are inline assembly like the V copies: the compiler counts
+// neither, and a load it counted would make it wait for the untracked copies
+// issued after it as well. kload_wait() waits for a buffer and ties the
+// buffer's registers to that wait, so nothing reads them earlier
+// (tests/test_isa_hazards.py checks the compiled code for it).
 constexpr int R8W = 1;                      // waves per work-group (LDS-bound occupancy)
 constexpr int R8T = 64 * R8W;
-constexpr int R8TILE = RSTEP * DH;          // bytes of one K or V code tile
-constexpr int R8SLOT = 2 * R8TILE;
-constexpr int R8NS = 2;                     // ring slots: steps in flight during a step's math
-constexpr int R8WAVE = R8NS * R8SLOT;
+constexpr int R8TILE = RSTEP * DH;          // bytes of one V code tile
+constexpr int R8P = 4;                      // steps in flight (K buffers, V ring slots)
+constexpr int R8WAVE = R8P * R8TILE;
 constexpr int R8LDS = R8W * R8WAVE;
 
 typedef int v2i32 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) v2i32 lds_v2i32;
+
+// One non-temporal global_load_dwordx4 into dst: 16 bytes at sbase + voff
+// (sbase wave-uniform). The compiler does not count it: the caller waits
+// with s_waitcnt and then passes dst through kload_wait before any use.
+// s_nop 4: the SGPR base may have been written by a VALU (v_readfirstlane)
+// just before, which a VMEM read of that SGPR must not follow within 5 wait
+// states.
+__device__ inline void kload(u32x4 &dst, const char *sbase, uint32_t voff) {
+  asm volatile("s_nop 4\n\tglobal_load_dwordx4 %0, %1, %2 nt"
+               : "=&v"(dst)
+               : "v"(voff), "s"(uniform_ptr(sbase))
+               : "memory");
+}
+// The same load from a per-lane address (the tail step re-reads the last
+// token for rows past the sequence).
+__device__ inline void kload(u32x4 &dst, const char *addr) {
+  asm volatile("global_load_dwordx4 %0, %1, off nt" : "=&v"(dst) : "v"(addr) : "memory");
+}
+// After the s_waitcnt that retired a buffer's loads: its registers are
+// produced here as far as the compiler knows, so no read of them (and no
+// copy) can be scheduled before the wait.
+// The statement emits only an assembly comment naming the registers, which
+// tests/test_isa_hazards.py matches against the loads' destinations (a copy
+// of a buffer before its wait would name other registers).
+__device__ inline void kload_wait(u32x4 (&k)[4]) {
+  asm volatile("; kload_wait %0 %1 %2 %3"
+               : "+v"(k[0]), "+v"(k[1]), "+v"(k[2]), "+v"(k[3])
+               :
+               : "memory");
+}
 
 template <bool PAGED>
 __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
@@ -455,7 +495,7 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
       *kb = *vb = (int64_t)tb * DH;
     }
   };
-  // DMA chunk c covers rows 8c .. 8c+7; this lane moves row 8c + lane/8,
+  // V copy chunk c covers rows 8c .. 8c+7; this lane moves row 8c + lane/8,
   // physical unit lane & 7
   uint32_t off[4];
 #pragma unroll
@@ -463,36 +503,46 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
     const int r = 8 * c + (lane >> 3);
     off[c] = (uint32_t)(r * tokb + (((lane & 7) ^ ((r >> 1) & 7)) << 4));
   }
-  auto issue = [&](int i) {
+  // K loads: row 16 kb + n, head_dim 64 sp + 16 G (q = 2 kb + sp)
+  uint32_t koff[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    koff[q] = (uint32_t)((16 * (q >> 1) + n) * tokb + 64 * (q & 1) + 16 * G);
+
+  u32x4 kq[R8P][4];  // K codes of the steps in flight, buffer i % R8P
+  // step i's K codes into buffer J (= i % R8P), then its V tile into ring
+  // slot J: 8 operations, always in this order
+  auto issue = [&](int i, auto J) {
+    constexpr int j = decltype(J)::value;
     const int tb = t0 + i * RSTEP;
-    const uint8_t *slot = ring + (i % R8NS) * R8SLOT;
+    const uint8_t *slot = ring + j * R8TILE;
     int64_t kb0, vb0;
     step_base(tb, &kb0, &vb0);
     if (tb + RSTEP <= Lb) {
       const char *kb = kbase + kb0, *vb = vbase + vb0;
 #pragma unroll
+      for (int q = 0; q < 4; ++q) kload(kq[j][q], kb, koff[q]);
+#pragma unroll
       for (int c = 0; c < 4; ++c) {
         // paged: the page base was read from the block table by v_readlane
         if constexpr (PAGED)
-          dma16<true>(kb, off[c], lds_offset(slot + c * 1024));
+          dma16<true>(vb, off[c], lds_offset(slot + c * 1024));
         else
-          dma16_sbase<true>(kb, off[c], lds_offset(slot + c * 1024));
-      }
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        if constexpr (PAGED)
-          dma16<true>(vb, off[c], lds_offset(slot + R8TILE + c * 1024));
-        else
-          dma16_sbase<true>(vb, off[c], lds_offset(slot + R8TILE + c * 1024));
+          dma16_sbase<true>(vb, off[c], lds_offset(slot + c * 1024));
       }
     } else {  // tail: rows past the sequence re-read its last token (masked)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = 16 * (q >> 1) + n;
+        const int64_t row = min(tb + r, Lb - 1) - tb;
+        kload(kq[j][q], kbase + kb0 + row * tokb + 64 * (q & 1) + 16 * G);
+      }
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int r = 8 * c + (lane >> 3);
         const int64_t row = min(tb + r, Lb - 1) - tb;
         const int u = ((lane & 7) ^ ((r >> 1) & 7)) << 4;
-        dma16<true>(kbase + kb0 + row * tokb + u, lds_offset(slot + c * 1024));
-        dma16<true>(vbase + vb0 + row * tokb + u, lds_offset(slot + R8TILE + c * 1024));
+        dma16<true>(vbase + vb0 + row * tokb + u, lds_offset(slot + c * 1024));
       }
     }
   };
@@ -511,7 +561,7 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
   // instead of a memory load; reloaded every 64 blocks. Paged, a block is a
   // page (one scale per page and kv head) and lane j holds the scales of
   // block-table entry blk0 + j: this window is separate from the copies'
-  // one, which runs up to two steps ahead of the math
+  // one, which runs up to R8P - 1 steps ahead of the math
   const int bsz = PAGED ? a.ps : a.sb;  // tokens per scale block
   int blk0 = 0;
   float kscv = 0.0f, vscv = 0.0f;
@@ -539,13 +589,15 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
   settle(kscv);
   settle(vscv);
   if (PAGED) settle(tabv);
-#pragma unroll
-  for (int i = 0; i < R8NS; ++i)
-    if (i < nsteps) issue(i);
-  // K reads: row n (+16 kb), logical unit 4 sp + G
-  int ka[2];
-#pragma unroll
-  for (int sp = 0; sp < 2; ++sp) ka[sp] = n * DH + (((4 * sp + G) ^ ((n >> 1) & 7)) << 4);
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  static_assert(R8P == 4, "the unrolled step loop below names four buffers");
+  if (0 < nsteps) issue(0, I0{});
+  if (1 < nsteps) issue(1, I1{});
+  if (2 < nsteps) issue(2, I2{});
+  if (3 < nsteps) issue(3, I3{});
   // V^T reads: source lane pair (2i, 2i+1) of group G names the token row of
   // k-slot i (keys 4 G + i, then 16 + 4 G + i - 4), 8 bytes each
   const int vi = (lane & 15) >> 1, vhalf = lane & 1;
@@ -558,18 +610,26 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
   for (int mb = 0; mb < 8; ++mb) oacc[mb] = f32x4{0, 0, 0, 0};
   float m = kNegFltMax, lsum = 0.0f;
 
-  for (int i = 0; i < nsteps; ++i) {
-    // this step's 8 copies have landed once only the later steps' may be
-    // outstanding (the next R8NS - 1 steps stay in flight during the math)
-    const int later = min(R8NS - 1, nsteps - 1 - i);
-    if (later >= 2)
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(16));
+  // waits until at most 8 * later + extra of this wave's operations are
+  // outstanding (later: steps issued after this one, each 8 operations)
+  auto wait_ops = [&](int later, auto extra) {
+    constexpr int X = decltype(extra)::value;
+    if (later >= 3)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(24 + X));
+    else if (later == 2)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(16 + X));
     else if (later == 1)
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(8));
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(8 + X));
     else
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-    const uint8_t *kt = ring + (i % R8NS) * R8SLOT;
-    const uint8_t *vt = kt + R8TILE;
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(X));
+  };
+  auto step = [&](int i, auto J) {
+    constexpr int j = decltype(J)::value;
+    const int later = min(R8P - 1, nsteps - 1 - i);
+    // K(i) has landed once only V(i) and the later steps may be outstanding
+    wait_ops(later, std::integral_constant<int, 4>{});
+    kload_wait(kq[j]);
+    const uint8_t *vt = ring + j * R8TILE;
     const int t = t0 + i * RSTEP;
 
     f32x4 s[2];
@@ -578,7 +638,7 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
       s[kb] = f32x4{0, 0, 0, 0};
 #pragma unroll
       for (int sp = 0; sp < 2; ++sp) {
-        const u32x4 c = *(const u32x4 *)(kt + kb * 16 * DH + ka[sp]);
+        const u32x4 c = kq[j][2 * kb + sp];
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2) {
           const u32x2 lo = e4m3x4_to_bf16(c[2 * h2]);
@@ -615,6 +675,8 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
     u32x4 pf;
 #pragma unroll
     for (int i2 = 0; i2 < 4; ++i2) pf[i2] = Bf16Tag::pack2(p[2 * i2] * vsc, p[2 * i2 + 1] * vsc);
+    // V(i) has landed once only the later steps may be outstanding
+    wait_ops(later, std::integral_constant<int, 0>{});
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) {
       const v2i32 c = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
@@ -624,13 +686,20 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
       const u32x4 A = {lo[0], lo[1], hi[0], hi[1]};
       oacc[mb] = Bf16Tag::mfma16(as_vec8<bf16x8>(A), as_vec8<bf16x8>(pf), oacc[mb]);
     }
+    // every read of this slot has returned before it is refilled
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-    if (i + R8NS < nsteps) issue(i + R8NS);
+    if (i + R8P < nsteps) issue(i + R8P, J);
     in_blk += RSTEP;
     if (in_blk == bsz) {
       in_blk = 0;
       ++blk;
     }
+  };
+  for (int i0 = 0; i0 < nsteps; i0 += R8P) {
+    step(i0, I0{});
+    if (i0 + 1 < nsteps) step(i0 + 1, I1{});
+    if (i0 + 2 < nsteps) step(i0 + 2, I2{});
+    if (i0 + 3 < nsteps) step(i0 + 3, I3{});
   }
 
   lsum += __shfl_xor(lsum, 16, 64);

@@ -81,9 +81,14 @@ def hazards(asm: str) -> list[str]:
     ins = _instructions(asm)
     found = []
     for j, (mnem, ops) in enumerate(ins):
-        if not mnem.startswith("global_load_lds"):
+        # the LDS copies (vaddr, saddr) and the register loads of the fp8 K
+        # codes (vdst, vaddr, saddr), both inline assembly
+        if mnem.startswith("global_load_lds"):
+            base = _sgprs(ops[1]) if len(ops) > 1 else set()
+        elif mnem == "global_load_dwordx4" and len(ops) > 2:
+            base = _sgprs(ops[2])
+        else:
             continue
-        base = _sgprs(ops[1]) if len(ops) > 1 else set()
         waits = 0
         for k in range(j - 1, -1, -1):
             pm, pops = ins[k]
@@ -101,6 +106,47 @@ def hazards(asm: str) -> list[str]:
             if waits >= VALU_SGPR_TO_VMEM:
                 break
     return found
+
+
+KLOAD = re.compile(r"^[ \t]*global_load_dwordx4 (v\[\d+:\d+\]), [^;\n]* nt[ \t]*$", re.M)
+KWAIT = re.compile(r";\s*kload_wait (v\[\d+:\d+\]) (v\[\d+:\d+\]) (v\[\d+:\d+\]) "
+                   r"(v\[\d+:\d+\])")
+
+
+def kload_findings(asm: str) -> tuple[int, list[str]]:
+    """The fp8 decode loads K codes into registers by inline assembly and
+    marks each wait for them with a "; kload_wait" comment naming the
+    registers its statement ties. Per kernel: every register quad a wait
+    names must be the destination of one of the kernel's K loads (a copy made
+    before the wait would name other registers and read data still in
+    flight), and the kernel must not spill (a spill store would read it
+    too). Returns (number of waits, findings)."""
+    found, waits = [], 0
+    for name, body in re.findall(r"^(\S+):\s*;\s*@\S+\n(.*?)^\.Lfunc_end", asm, re.S | re.M):
+        dests = set(KLOAD.findall(body))
+        named = [q for m in KWAIT.findall(body) for q in m]
+        if not named:
+            continue
+        waits += len(named) // 4
+        for q in named:
+            if q not in dests:
+                found.append(f"{name}: kload_wait names {q}, which no K load writes")
+        if re.search(r"^\s*(scratch_|buffer_store)", body, re.M):
+            found.append(f"{name}: spills while K loads are in flight")
+    return waits, found
+
+
+def test_kload_checker_flags_a_copy():
+    ok = ("k:  ; @k\n\tglobal_load_dwordx4 v[18:21], v140, s[20:21] nt\n"
+          "\t; kload_wait v[18:21] v[22:25] v[26:29] v[30:33]\n.Lfunc_end0:\n")
+    loads = "".join(f"\tglobal_load_dwordx4 v[{a}:{a + 3}], v140, s[20:21] nt\n"
+                    for a in (22, 26, 30))
+    good = ok.replace("\t; kload", loads + "\t; kload")
+    assert kload_findings(good) == (1, [])
+    copied = good.replace("kload_wait v[18:21]", "kload_wait v[40:43]")
+    assert len(kload_findings(copied)[1]) == 1
+    spilled = good.replace("\t; kload", "\tscratch_store_dwordx4 off, v[18:21], s33\n\t; kload")
+    assert len(kload_findings(spilled)[1]) == 1
 
 
 def test_checker_flags_a_stale_base():
@@ -124,12 +170,16 @@ def test_lds_dma_wait_states(tmp_path):
         procs[src.name] = (out, subprocess.Popen(
             [HIPCC, *flags, "--cuda-device-only", "-S", "-o", str(out), str(src)],
             stdout=subprocess.DEVNULL, stderr=subprocess.PIPE, text=True))
-    report, copies = [], 0
+    report, copies, kwaits = [], 0, 0
     for name, (out, p) in procs.items():
         _, err = p.communicate(timeout=600)
         assert p.returncode == 0, f"{name}: {err[-2000:]}"
         asm = out.read_text()
         copies += asm.count("global_load_lds_dwordx4")
         report += [f"{name}: {h}" for h in hazards(asm)]
+        n, found = kload_findings(asm)
+        kwaits += n
+        report += [f"{name}: {f}" for f in found]
     assert copies > 0, "no LDS DMA copies found: the checker is looking at the wrong code"
+    assert kwaits > 0, "no K-load waits found: the checker is looking at the wrong code"
     assert not report, "\n".join(report)
