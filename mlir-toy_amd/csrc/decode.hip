@@ -24,6 +24,7 @@
 // measured ~10% more HBM bandwidth for this stream.
 #include <mutex>
 #include <type_traits>
+#include <utility>
 
 #include "device_common.h"
 #include "kernels.h"
@@ -410,6 +411,16 @@ constexpr int R8LDS = R8W * R8WAVE;
 typedef int v2i32 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) v2i32 lds_v2i32;
 
+// f(std::integral_constant<int, 0>{}) .. f(std::integral_constant<int, N - 1>{})
+template <int N, class F, int... I>
+__device__ inline void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ inline void static_for(F &&f) {
+  static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
+}
+
 // One non-temporal global_load_dwordx4 into dst: 16 bytes at sbase + voff
 // (sbase wave-uniform). The compiler does not count it: the caller waits
 // with s_waitcnt and then passes dst through kload_wait before any use.
@@ -589,15 +600,9 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
   settle(kscv);
   settle(vscv);
   if (PAGED) settle(tabv);
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
-  using I3 = std::integral_constant<int, 3>;
-  static_assert(R8P == 4, "the unrolled step loop below names four buffers");
-  if (0 < nsteps) issue(0, I0{});
-  if (1 < nsteps) issue(1, I1{});
-  if (2 < nsteps) issue(2, I2{});
-  if (3 < nsteps) issue(3, I3{});
+  static_for<R8P>([&](auto J) {
+    if (decltype(J)::value < nsteps) issue(decltype(J)::value, J);
+  });
   // V^T reads: source lane pair (2i, 2i+1) of group G names the token row of
   // k-slot i (keys 4 G + i, then 16 + 4 G + i - 4), 8 bytes each
   const int vi = (lane & 15) >> 1, vhalf = lane & 1;
@@ -614,14 +619,11 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
   // outstanding (later: steps issued after this one, each 8 operations)
   auto wait_ops = [&](int later, auto extra) {
     constexpr int X = decltype(extra)::value;
-    if (later >= 3)
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(24 + X));
-    else if (later == 2)
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(16 + X));
-    else if (later == 1)
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(8 + X));
-    else
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(X));
+    static_assert(8 * (R8P - 1) + X <= 63, "vmcnt holds at most 63");
+    static_for<R8P>([&](auto L) {
+      constexpr int l = decltype(L)::value;
+      if (later == l) __builtin_amdgcn_s_waitcnt(waitcnt_vm(8 * l + X));
+    });
   };
   auto step = [&](int i, auto J) {
     constexpr int j = decltype(J)::value;
@@ -695,12 +697,10 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
       ++blk;
     }
   };
-  for (int i0 = 0; i0 < nsteps; i0 += R8P) {
-    step(i0, I0{});
-    if (i0 + 1 < nsteps) step(i0 + 1, I1{});
-    if (i0 + 2 < nsteps) step(i0 + 2, I2{});
-    if (i0 + 3 < nsteps) step(i0 + 3, I3{});
-  }
+  for (int i0 = 0; i0 < nsteps; i0 += R8P)
+    static_for<R8P>([&](auto J) {
+      if (i0 + decltype(J)::value < nsteps) step(i0 + decltype(J)::value, J);
+    });
 
   lsum += __shfl_xor(lsum, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);

@@ -83,7 +83,9 @@ def hazards(asm: str) -> list[str]:
     for j, (mnem, ops) in enumerate(ins):
         # the LDS copies (vaddr, saddr) and the register loads of the fp8 K
         # codes (vdst, vaddr, saddr), both inline assembly
-        if mnem.startswith("global_load_lds"):
+        # (only the LDS copies read M0)
+        reads_m0 = mnem.startswith("global_load_lds")
+        if reads_m0:
             base = _sgprs(ops[1]) if len(ops) > 1 else set()
         elif mnem == "global_load_dwordx4" and len(ops) > 2:
             base = _sgprs(ops[2])
@@ -99,7 +101,8 @@ def hazards(asm: str) -> list[str]:
                 found.append(f"copy #{j} ({' '.join([mnem] + ops)}): base written by "
                              f"{pm} {', '.join(pops)} {waits} wait states before")
                 break
-            if pm.startswith("s_") and pops and pops[0] == "m0" and waits < M0_TO_LDS_DMA:
+            if (reads_m0 and pm.startswith("s_") and pops and pops[0] == "m0"
+                    and waits < M0_TO_LDS_DMA):
                 found.append(f"copy #{j}: M0 written by {pm} {waits} wait states before")
                 break
             waits += 1
@@ -159,6 +162,8 @@ def test_checker_flags_a_stale_base():
     assert len(hazards(bad)) == 1
     assert hazards(good) == []
     assert len(hazards(m0)) == 1 and hazards(m0.replace("\tglobal", "\ts_nop 0\n\tglobal")) == []
+    # a register load does not read M0
+    assert hazards("\ts_mov_b32 m0, s4\n\tglobal_load_dwordx4 v[4:7], v[2:3], off\n") == []
 
 
 @pytest.mark.skipif(not Path(HIPCC).exists(), reason="hipcc not available")
