@@ -106,8 +106,10 @@ def spin_up(fn, seconds, rotate=1):
 
 def time_launches(fn, steps, warmup, rotate=1, spinup=None):
     """Spin up, run warmup + steps launches; returns (wall seconds for the
-    timed steps, mean per-launch seconds from HIP events on the current
-    stream)."""
+    timed steps, mean seconds per step from one pair of HIP events around
+    the timed steps on the current stream). The steps run back to back, as
+    a serving loop issues them: a timing marker between steps would add its
+    own dispatch latency (some 5 us) to every step."""
     import torch
 
     spinup = SPINUP_S if spinup is None else spinup
@@ -116,16 +118,16 @@ def time_launches(fn, steps, warmup, rotate=1, spinup=None):
     for i in range(warmup):
         fn(i % rotate)
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    stops = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    start.record()
     for i in range(steps):
-        starts[i].record()
         fn(i % rotate)
-        stops[i].record()
+    stop.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ev = sum(a.elapsed_time(b) for a, b in zip(starts, stops)) / steps / 1e3
+    ev = start.elapsed_time(stop) / steps / 1e3
     return wall, ev
 
 

@@ -741,10 +741,14 @@ __global__ __launch_bounds__(R8T) void decode_partial_ring8(DecArgs a) {
 }
 
 // One work-group per (batch, query head): combine the splits' partials.
-// Wave 0 reads every split's (m, l) at once (one lane per split), reduces
-// M and L across the wave and leaves the weights 2^(m_s - M) in LDS; then
-// every thread (one head_dim element) sums its splits' o~ with the loads
-// unrolled so they are in flight together.
+// Every thread (one head_dim element) first issues the loads of its first
+// kCombinePre splits' o~, which do not depend on the weights, so their
+// latency overlaps that of the (m, l) reads. Wave 0 reads every split's
+// (m, l) (one lane per split), reduces M and L across the wave and leaves
+// the weights 2^(m_s - M) in LDS; then each thread sums its splits' o~ in
+// split order.
+constexpr int kCombinePre = 16;
+
 __global__ __launch_bounds__(DH) void decode_combine(const float *part_o,
                                                      const float *part_ml,
                                                      uint16_t *o, float *lse,
@@ -754,6 +758,10 @@ __global__ __launch_bounds__(DH) void decode_combine(const float *part_o,
   const int64_t bh = blockIdx.x;
   const int d = threadIdx.x;
   const float *ml = part_ml + bh * splits * 2;
+  const float *po = part_o + bh * splits * DH + d;
+  float pre[kCombinePre];
+#pragma unroll
+  for (int s = 0; s < kCombinePre; ++s) pre[s] = s < splits ? po[(int64_t)s * DH] : 0.0f;
   if (d < 64) {
     float M = kNegFltMax;
     for (int s = d; s < splits; s += 64) M = fmaxf(M, ml[2 * s]);
@@ -773,10 +781,12 @@ __global__ __launch_bounds__(DH) void decode_combine(const float *part_o,
     }
   }
   __syncthreads();
-  const float *po = part_o + bh * splits * DH + d;
   float acc = 0.0f;
+#pragma unroll
+  for (int s = 0; s < kCombinePre; ++s)
+    if (s < splits) acc += wts[s] * pre[s];
 #pragma unroll 8
-  for (int s = 0; s < splits; ++s) acc += wts[s] * po[(int64_t)s * DH];
+  for (int s = kCombinePre; s < splits; ++s) acc += wts[s] * po[(int64_t)s * DH];
   const float Ls = stat[1];
   // an empty sequence (paged decode with length 0) has L = 0: O = 0, lse = -inf
   o[bh * DH + d] = Bf16Tag::from_f32(Ls > 0.0f ? acc / Ls : 0.0f);
