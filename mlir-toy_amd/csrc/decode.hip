@@ -954,29 +954,15 @@ hipError_t launch_decode(const DecodeLaunch &L, hipStream_t s) {
   a.v_ps[0] = L.v_pstride[0];
   a.v_ps[1] = L.v_pstride[1];
   const int grid = (int)(L.batch * L.heads_kv * L.splits);
-  // Each kernel's dynamic-LDS limit is set once per process (function-local
-  // statics are initialised exactly once, also under concurrent first calls);
-  // a failure is kept and returned by every later launch.
+  // Both rings fit the dynamic LDS every launch may use without a per-kernel
+  // attribute (which would have to be set on each device), so none is set.
+  static_assert(RLDS <= 48 * 1024 && R8LDS <= 48 * 1024, "decode ring past the default LDS limit");
   if (L.kv_dtype == 3) {
-    static const hipError_t attr8_c = hipFuncSetAttribute(
-        (const void *)decode_partial_ring8<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-        R8LDS);
-    static const hipError_t attr8_p = hipFuncSetAttribute(
-        (const void *)decode_partial_ring8<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-        R8LDS);
-    const hipError_t attr8 = paged ? attr8_p : attr8_c;
-    if (attr8 != hipSuccess) return attr8;
     if (paged)
       hipLaunchKernelGGL(decode_partial_ring8<true>, dim3(grid), dim3(R8T), R8LDS, s, a);
     else
       hipLaunchKernelGGL(decode_partial_ring8<false>, dim3(grid), dim3(R8T), R8LDS, s, a);
   } else {
-    static const hipError_t attr_c = hipFuncSetAttribute(
-        (const void *)decode_partial_ring<false>, hipFuncAttributeMaxDynamicSharedMemorySize, RLDS);
-    static const hipError_t attr_p = hipFuncSetAttribute(
-        (const void *)decode_partial_ring<true>, hipFuncAttributeMaxDynamicSharedMemorySize, RLDS);
-    const hipError_t attr = paged ? attr_p : attr_c;
-    if (attr != hipSuccess) return attr;
     if (paged)
       hipLaunchKernelGGL(decode_partial_ring<true>, dim3(grid), dim3(RT), RLDS, s, a);
     else
