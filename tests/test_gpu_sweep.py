@@ -67,7 +67,7 @@ def _prefill_case(i):
                 stages=stages, kd=kd, strided=strided, seed=1000 + i)
 
 
-@pytest.mark.parametrize("i", range(40))
+@pytest.mark.parametrize("i", range(200))
 def test_prefill_sweep(ops, i):
     c = _prefill_case(i)
     _log(f"case: prefill sweep {c}")
@@ -112,7 +112,7 @@ def _decode_case(i):
     return dict(B=B, Hq=Hk * group, Hk=Hk, L=L, splits=splits, fp8=fp8, sb=sb, seed=2000 + i)
 
 
-@pytest.mark.parametrize("i", range(24))
+@pytest.mark.parametrize("i", range(120))
 def test_decode_sweep(ops, i):
     c = _decode_case(i)
     _log(f"case: decode sweep {c}")
@@ -161,7 +161,7 @@ def _paginate(kv, ps, rng, token_major):
     return (view.permute(0, 2, 1, 3) if token_major else view), ids.cuda()
 
 
-@pytest.mark.parametrize("i", range(16))
+@pytest.mark.parametrize("i", range(80))
 def test_paged_decode_sweep(ops, i):
     rng = np.random.default_rng(3000 + i)
     B = int(rng.integers(1, 4))
