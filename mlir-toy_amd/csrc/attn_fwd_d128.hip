@@ -320,45 +320,52 @@ __global__ __launch_bounds__(NT, STAGES == 3 ? 1 : 2) void attn_fwd_d128(AttnArg
   const float sc = a.scale2;
   const f32x16 zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
-  auto qk = [&](const uint8_t *kt) {
+  // The A operand of MFMA i = 2 st + kb of S^T = K.Q^T (32 keys x 16 head_dim)
+  auto k_operand = [&](const uint8_t *kt, int i) {
+    const int st = i >> 1, kb = i & 1;
     if constexpr (KT) {
-#pragma unroll
-      for (int st = 0; st < 8; ++st)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          const v4i16 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_v4i16 *)as_lds(kt + (16 * st) * 128 + kta[kb]));
-          const v4i16 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_v4i16 *)as_lds(kt + (16 * st + 8) * 128 + kta[kb]));
-          const u32x2 a0 = __builtin_bit_cast(u32x2, t0), a1 = __builtin_bit_cast(u32x2, t1);
-          const u32x4 A = {a0[0], a0[1], a1[0], a1[1]};
-          s[kb] = E::mfma32(as_vec8<V8>(A), as_vec8<V8>(qf[st]), st == 0 ? zero16 : s[kb]);
-        }
-      // two transpose reads per MFMA, issued two MFMAs ahead
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
-#pragma unroll
-      for (int i = 0; i < 14; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
+      const v4i16 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_v4i16 *)as_lds(kt + (16 * st) * 128 + kta[kb]));
+      const v4i16 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_v4i16 *)as_lds(kt + (16 * st + 8) * 128 + kta[kb]));
+      const u32x2 a0 = __builtin_bit_cast(u32x2, t0), a1 = __builtin_bit_cast(u32x2, t1);
+      return u32x4{a0[0], a0[1], a1[0], a1[1]};
     } else {
-#pragma unroll
-      for (int st = 0; st < 8; ++st)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          const u32x4 A = *(const u32x4 *)(kt + kb * 8192 + ka[st]);
-          s[kb] = E::mfma32(as_vec8<V8>(A), as_vec8<V8>(qf[st]), st == 0 ? zero16 : s[kb]);
-        }
-      // operand reads run two MFMAs ahead (bounds the live registers)
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
-#pragma unroll
-      for (int i = 0; i < 14; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
+      return *(const u32x4 *)(kt + kb * 8192 + ka[st]);
     }
+  };
+  // S^T of one key block, its first two A operands already read (k0, k1):
+  // the caller issues those reads early, so the MFMA stream does not start
+  // with an LDS round trip
+  auto qk_from = [&](const uint8_t *kt, const u32x4 &k0, const u32x4 &k1) {
+#pragma unroll
+    for (int st = 0; st < 8; ++st)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int i = 2 * st + kb;
+        const u32x4 A = i == 0 ? k0 : i == 1 ? k1 : k_operand(kt, i);
+        s[kb] = E::mfma32(as_vec8<V8>(A), as_vec8<V8>(qf[st]), st == 0 ? zero16 : s[kb]);
+      }
+    // the remaining operand reads run two MFMAs ahead
+    constexpr int R = KT ? 2 : 1;  // LDS reads per operand
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * R, 1);
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, R, 1);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
+  };
+  auto qk = [&](const uint8_t *kt) { qk_from(kt, k_operand(kt, 0), k_operand(kt, 1)); };
+  // The A operand of P.V step st (V^T: head_dim rows 32 nb .., keys 16 c ..)
+  auto v_operand = [&](const uint8_t *vt, int st) {
+    const int c = st >> 2, nb = st & 3;
+    const v4i16 t0 =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)as_lds(vt + (16 * c) * 256 + va[nb]));
+    const v4i16 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_v4i16 *)as_lds(vt + (16 * c + 8) * 256 + va[nb]));
+    const u32x2 a0 = __builtin_bit_cast(u32x2, t0), a1 = __builtin_bit_cast(u32x2, t1);
+    return u32x4{a0[0], a0[1], a1[0], a1[1]};
   };
 
   // O = acc / l rounded to the input type (HTile:130-143) and the LSE. The
@@ -416,6 +423,11 @@ __global__ __launch_bounds__(NT, STAGES == 3 ? 1 : 2) void attn_fwd_d128(AttnArg
     }
     const int qrow0 = qbs[item] * BM + w * 32;
     if (jb < nkw[item]) {
+      // the first two V^T operands of this block's P.V, read before the
+      // softmax (the V tile landed in the previous iteration)
+      const uint8_t *vt = vslot(vb);
+      const u32x4 vp0 = v_operand(vt, 0), vp1 = v_operand(vt, 1);
+      u32x4 kn0, kn1;
       const int key0 = jb * BN;
       const bool need_mask = (key0 + BN > a.Sk) || (CAUSAL && key0 + BN - 1 > qrow0 + a.off);
       if (need_mask) {
@@ -486,35 +498,38 @@ __global__ __launch_bounds__(NT, STAGES == 3 ? 1 : 2) void attn_fwd_d128(AttnArg
       }
       lsum += rs;
 
-      // O^T += V^T P^T for this block (A operand by transpose reads). The
-      // wave raises its issue priority for its MFMA stretch so the matrix
-      // core is fed first while the other wave on the SIMD runs its softmax.
+      // O^T += V^T P^T for this block (A operand by transpose reads; the
+      // first two were read before the softmax). The wave raises its issue
+      // priority for its MFMA stretch so the matrix core is fed first while
+      // the other wave on the SIMD runs its softmax.
       __builtin_amdgcn_s_setprio(1);
-      const uint8_t *vt = vslot(vb);
 #pragma unroll
       for (int step = 0; step < 16; ++step) {
         const int c = step >> 2, nb = step & 3;
-        const v4i16 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_v4i16 *)as_lds(vt + (16 * c) * 256 + va[nb]));
-        const v4i16 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_v4i16 *)as_lds(vt + (16 * c + 8) * 256 + va[nb]));
-        const u32x2 a0 = __builtin_bit_cast(u32x2, t0), a1 = __builtin_bit_cast(u32x2, t1);
-        const u32x4 A = {a0[0], a0[1], a1[0], a1[1]};
+        const u32x4 A = step == 0 ? vp0 : step == 1 ? vp1 : v_operand(vt, step);
         o[nb] = E::mfma32(as_vec8<V8>(A), as_vec8<V8>(pf[c]), o[nb]);
+      }
+      // the next block's first two K operands (its K tile arrived during
+      // the previous iteration; a block with no next one reads a stale
+      // slot and drops the values), so its S^T starts without a round trip
+      if constexpr (STAGES > 1) {
+        kn0 = k_operand(kslot(vb + 1), 0);
+        kn1 = k_operand(kslot(vb + 1), 1);
       }
       // reads run two MFMAs ahead
       __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-      for (int i = 0; i < 14; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      for (int i = 0; i < 12; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       }
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, KT ? 4 : 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
 
-      // S^T of the next block of this query block (its K tile arrived
-      // during the previous iteration)
+      // S^T of the next block of this query block
       if constexpr (STAGES > 1)
-        if (jb + 1 < nkw[item]) qk(kslot(vb + 1));
+        if (jb + 1 < nkw[item]) qk_from(kslot(vb + 1), kn0, kn1);
       __builtin_amdgcn_s_setprio(0);
     }
     if constexpr (STAGES == 1) {
