@@ -406,6 +406,30 @@ def bench_copy(torch, steps, warmup, nbytes=1 << 30):
     return "copy 1 GiB", wall, ev, 2 * nbytes, None
 
 
+def bench_gemm(torch, steps, warmup, n=8192):
+    """A bf16 n^3 GEMM through torch.matmul (hipBLASLt): the vendor's own dense
+    MFMA rate on this box, under the same power cap as the prefill. It
+    calibrates what fraction of the nominal MFMA peak dense bf16 work reaches
+    here; not part of the default run."""
+    a = torch.randn((n, n), device="cuda").to(torch.bfloat16)
+    b = torch.randn((n, n), device="cuda").to(torch.bfloat16)
+    c = torch.empty((n, n), device="cuda", dtype=torch.bfloat16)
+    wall, ev = time_launches(lambda _: torch.matmul(a, b, out=c), steps, warmup)
+    return f"bf16 GEMM {n}^3 (torch.matmul, hipBLASLt)", wall, ev, 2.0 * n ** 3, None
+
+
+def mfma_entry(name, wall, ev, flops, steps):
+    tf = flops / ev / 1e12
+    return {
+        "workload": name,
+        "value": round(flops * steps / wall / 1e12, 1),
+        "unit": "TFLOP/s",
+        "us_per_step": round(ev * 1e6, 2),
+        "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None},
+    }
+
+
 def hbm_entry(key, name, wall, ev, nbytes, steps, traffic, cpu=None):
     gbs = nbytes / ev / 1e9
     return {
@@ -465,9 +489,10 @@ def main():
                     help="skip the decode/scan configurations")
     ap.add_argument("--workload", default="all",
                     choices=["all", "prefill", "decode", "decode_fp8", "decode_paged",
-                             "decode_paged_fp8", "scan", "config1", "copy"],
+                             "decode_paged_fp8", "scan", "config1", "copy", "gemm"],
                     help="run one configuration only (for profiling); 'copy' is a plain "
-                         "1 GiB device copy used to calibrate HBM byte counters")
+                         "1 GiB device copy used to calibrate HBM byte counters, 'gemm' a "
+                         "bf16 8192^3 torch.matmul that calibrates the dense MFMA rate")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--spinup", type=float, default=SPINUP_S,
                     help="untimed seconds of each workload before its warmup steps "
@@ -506,14 +531,17 @@ def main():
                                                        fp8=True),
         "scan": lambda: bench_scan(ops, torch, args.steps, args.warmup),
         "copy": lambda: bench_copy(torch, args.steps, args.warmup),
+        "gemm": lambda: bench_gemm(torch, args.steps, args.warmup),
         "config1": lambda: bench_config1(ops, torch, args.steps, args.warmup),
     }
     if args.workload in single:
         name, wall, ev, work, cpu = single[args.workload]()
-        make = config1_entry if args.workload == "config1" else \
-            lambda *a, **kw: hbm_entry(args.workload, *a, **kw)
-        entry = make(name, wall, ev, work, args.steps, **({} if args.workload == "config1"
-                                                          else {"traffic": traffic}))
+        if args.workload == "config1":
+            entry = config1_entry(name, wall, ev, work, args.steps)
+        elif args.workload == "gemm":
+            entry = mfma_entry(name, wall, ev, work, args.steps)
+        else:
+            entry = hbm_entry(args.workload, name, wall, ev, work, args.steps, traffic)
         if args.workload == "scan":
             entry["roofline_valu"] = scan_valu_roofline(ev)
         print(json.dumps(entry), flush=True)
