@@ -255,6 +255,82 @@ int run_decode(const std::string &dir) {
   return g_failures ? 1 : 0;
 }
 
+int run_fp8(const std::string &dir) {
+  auto m = read_meta(dir);
+  neptune_decode_desc d = decode_desc((int64_t)m["batch"], (int64_t)m["heads_q"],
+                                      (int64_t)m["heads_kv"], (int64_t)m["seq_kv"],
+                                      (int64_t)m["num_splits"]);
+  d.kv_dtype = NEPTUNE_DTYPE_FP8_E4M3;
+  d.scale_block = (int64_t)m["scale_block"];
+  const auto q = read_array<uint16_t>(dir + "/q.bin");
+  const auto k = read_array<uint8_t>(dir + "/k.bin"), v = read_array<uint8_t>(dir + "/v.bin");
+  const auto ks = read_array<float>(dir + "/k_scale.bin"),
+             vs = read_array<float>(dir + "/v_scale.bin");
+  const auto want_o = read_array<float>(dir + "/o.bin"),
+             want_lse = read_array<float>(dir + "/lse.bin");
+  size_t ws_bytes = 0;
+  expect(neptune_decode_workspace_bytes(&d, &ws_bytes) == NEPTUNE_OK, "fp8: workspace bytes");
+  DeviceBuffer dq(q), dk(k), dv(v), dks(ks), dvs(vs), ws(ws_bytes), o1(q.size() * 2),
+      o2(q.size() * 2), l1(want_lse.size() * 4), l2(want_lse.size() * 4);
+  expect(neptune_decode_splitk(&d, dq.ptr, dk.ptr, dv.ptr, (const float *)dks.ptr,
+                               (const float *)dvs.ptr, o1.ptr, (float *)l1.ptr, ws.ptr, ws_bytes,
+                               nullptr) == NEPTUNE_OK,
+         "fp8: decode_splitk status");
+  expect(neptune_decode_splitk_noalloc(&d, dq.ptr, dk.ptr, dv.ptr, (const float *)dks.ptr,
+                                       (const float *)dvs.ptr, o2.ptr, (float *)l2.ptr,
+                                       nullptr) == NEPTUNE_OK,
+         "fp8: decode_splitk_noalloc status");
+  hip_ok(hipDeviceSynchronize(), "sync");
+  const auto got1 = o1.to_host<uint16_t>(), got2 = o2.to_host<uint16_t>();
+  const auto lse1 = l1.to_host<float>(), lse2 = l2.to_host<float>();
+  double ref_max = 0.0;
+  for (float x : want_o) ref_max = std::fmax(ref_max, std::fabs((double)x));
+  const double eo = max_err_bf16(got1, want_o), el = max_err_f32(lse1, want_lse);
+  expect(eo <= m["tol"] && eo <= m["tol"] * ref_max, "fp8: output within tolerance");
+  expect(el <= 1e-3, "fp8: lse within 1e-3");
+  expect(got1 == got2 && std::memcmp(lse1.data(), lse2.data(), lse1.size() * 4) == 0,
+         "fp8: noalloc bit-identical to the workspace entry point");
+  std::printf("fp8: %s max|o-ref|=%.3e (max|ref| %.3e) max|lse-ref|=%.3e\n",
+              g_failures ? "FAILED" : "ok", eo, ref_max, el);
+  return g_failures ? 1 : 0;
+}
+
+int run_scan(const std::string &dir) {
+  auto m = read_meta(dir);
+  neptune_scan_desc sd;
+  std::memset(&sd, 0, sizeof sd);
+  sd.batch = (int64_t)m["batch"];
+  sd.dim = (int64_t)m["dim"];
+  sd.seq_len = (int64_t)m["seq_len"];
+  sd.d_state = (int64_t)m["d_state"];
+  sd.io_dtype = NEPTUNE_DTYPE_BF16;
+  sd.delta_softplus = 1;
+  const auto u = read_array<uint16_t>(dir + "/u.bin"), dr = read_array<uint16_t>(dir + "/delta.bin"),
+             Bm = read_array<uint16_t>(dir + "/B.bin"), Cm = read_array<uint16_t>(dir + "/C.bin"),
+             z = read_array<uint16_t>(dir + "/z.bin");
+  const auto A = read_array<float>(dir + "/A.bin"), D = read_array<float>(dir + "/D.bin"),
+             bias = read_array<float>(dir + "/delta_bias.bin"),
+             want = read_array<float>(dir + "/y.bin");
+  DeviceBuffer du(u), ddr(dr), dB(Bm), dC(Cm), dz(z), dA(A), dD(D), dbias(bias),
+      dy(u.size() * 2);
+  expect(neptune_selective_scan_fwd(&sd, du.ptr, ddr.ptr, (const float *)dA.ptr, dB.ptr, dC.ptr,
+                                    (const float *)dD.ptr, dz.ptr, (const float *)dbias.ptr,
+                                    dy.ptr, nullptr) == NEPTUNE_OK,
+         "scan: status");
+  hip_ok(hipDeviceSynchronize(), "sync");
+  const auto got = dy.to_host<uint16_t>();
+  // |a - b| <= 2e-2 * max(1, |ref|), elementwise
+  double worst = 0.0;
+  for (size_t i = 0; i < want.size(); ++i) {
+    const double err = std::fabs((double)bf16_to_f32(got[i]) - (double)want[i]);
+    worst = std::fmax(worst, err / std::fmax(1.0, std::fabs((double)want[i])));
+  }
+  expect(worst <= 2e-2, "scan: y within 2e-2 * max(1, |ref|)");
+  std::printf("scan: %s max |y-ref| / max(1,|ref|) = %.3e\n", g_failures ? "FAILED" : "ok",
+              worst);
+  return g_failures ? 1 : 0;
+}
+
 }  // namespace
 
 int main(int argc, char **argv) {
@@ -262,6 +338,9 @@ int main(int argc, char **argv) {
   if (mode == "validate") return run_validate();
   if (mode == "attn" && argc > 2) return run_attn(argv[2]);
   if (mode == "decode" && argc > 2) return run_decode(argv[2]);
-  std::fprintf(stderr, "usage: %s validate | attn DIR | decode DIR\n", argv[0]);
+  if (mode == "fp8" && argc > 2) return run_fp8(argv[2]);
+  if (mode == "scan" && argc > 2) return run_scan(argv[2]);
+  std::fprintf(stderr, "usage: %s validate | attn DIR | decode DIR | fp8 DIR | scan DIR\n",
+               argv[0]);
   return 2;
 }

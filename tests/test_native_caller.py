@@ -5,10 +5,13 @@ the results itself, as a C++ runtime embedding the backend would (the
 reference's plugin host finds its extern "C" entry by dlopen,
 lib/HTile/HTileDialect.cpp:27-37).
 
-On the CPU it exercises the host-side validation and the no-device path; on
-the GPU it runs neptune_attn_fwd on the attn_bf16_causal_gqa fixture and
-neptune_decode_splitk / neptune_decode_splitk_noalloc on decode_bf16_gqa,
-whose expected outputs are the fixtures' float64 closed forms."""
+On the CPU it exercises the host-side validation and the no-device path.
+On the GPU it runs:
+- neptune_attn_fwd on the attn_bf16_causal_gqa fixture;
+- neptune_decode_splitk and neptune_decode_splitk_noalloc on decode_bf16_gqa
+  and, with fp8 KV, on decode_fp8;
+- neptune_selective_scan_fwd on scan_small.
+The expected outputs are the fixtures' float64 closed forms."""
 
 import os
 import subprocess
@@ -81,3 +84,40 @@ def test_native_caller_decode_fixture(tmp_path):
     r = _run("decode", tmp_path)
     assert r.returncode == 0, r.stderr
     assert "decode: ok" in r.stdout
+
+
+@pytest.mark.gpu
+def test_native_caller_fp8_decode_fixture(tmp_path):
+    """fp8-E4M3 KV with per-block scales through both decode entry points;
+    the expected output is the fixture's float64 closed form on the same
+    codes and scales."""
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    g = load("decode_fp8")
+    B, Hq, _ = g["q"].shape
+    Hk, L = g["k_codes"].shape[1], g["k_codes"].shape[2]
+    _write(tmp_path, dict(batch=B, heads_q=Hq, heads_kv=Hk, seq_kv=L,
+                          num_splits=int(g["num_splits"]), scale_block=int(g["scale_block"]),
+                          tol=TOL_BF16_ABS),
+           dict(q=g["q"], k=g["k_codes"], v=g["v_codes"], k_scale=g["k_scale"],
+                v_scale=g["v_scale"], o=g["o"].astype(np.float32),
+                lse=g["lse"].astype(np.float32)))
+    r = _run("fp8", tmp_path)
+    assert r.returncode == 0, r.stderr
+    assert "fp8: ok" in r.stdout
+
+
+@pytest.mark.gpu
+def test_native_caller_scan_fixture(tmp_path):
+    """The selective scan with D, z and delta_bias (softplus on), against the
+    fixture's float64 recurrence."""
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    g = load("scan_small")
+    b, d, L = g["u"].shape
+    _write(tmp_path, dict(batch=b, dim=d, seq_len=L, d_state=g["A"].shape[1]),
+           {k: g[k] for k in ("u", "delta", "B", "C", "z", "A", "D", "delta_bias")} |
+           dict(y=g["y"].astype(np.float32)))
+    r = _run("scan", tmp_path)
+    assert r.returncode == 0, r.stderr
+    assert "scan: ok" in r.stdout
