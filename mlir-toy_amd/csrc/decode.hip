@@ -411,16 +411,6 @@ constexpr int R8LDS = R8W * R8WAVE;
 typedef int v2i32 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) v2i32 lds_v2i32;
 
-// f(std::integral_constant<int, 0>{}) .. f(std::integral_constant<int, N - 1>{})
-template <int N, class F, int... I>
-__device__ inline void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, class F>
-__device__ inline void static_for(F &&f) {
-  static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
-}
-
 // One non-temporal global_load_dwordx4 into dst: 16 bytes at sbase + voff
 // (sbase wave-uniform). The compiler does not count it: the caller waits
 // with s_waitcnt and then passes dst through kload_wait before any use.

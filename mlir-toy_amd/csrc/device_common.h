@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace neptune {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -70,6 +72,17 @@ struct F16Tag {
 template <class V>
 __device__ inline V as_vec8(u32x4 u) {
   return __builtin_bit_cast(V, u);
+}
+
+// f(std::integral_constant<int, 0>{}) .. f(std::integral_constant<int, N - 1>{}),
+// in order: a loop whose index is a constant expression in the body
+template <class F, int... I>
+__device__ inline void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ inline void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 // v_exp_f32: 2^x, flushes denormal results; exp2(-inf) = 0.

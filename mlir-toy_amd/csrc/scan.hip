@@ -7,34 +7,46 @@
 //   x_n  <- 2^(delta * A[d,n] * log2 e) x_n + (delta u) B[b,n,l]
 //   y     = (sum_n C[b,n,l] x_n + D[d] u) * silu(z)
 //
-// The per-state update (one exp2, two multiplies, one FMA, one multiply for
-// the output term) is VALU/transcendental work: 16 states per (channel,
-// step) against 8 bytes of HBM traffic, so the kernel is bound by the VALU,
-// not by HBM. The design therefore maximises the number of independent
-// wavefronts per SIMD and keeps every other cost off the VALU:
+// The per-state update (one exp2, two multiplies, one FMA) and the output
+// term (one FMA per state) are VALU/transcendental work: 16 states per
+// (channel, step) against 8 bytes of HBM traffic, so the kernel is bound by
+// the VALU, not by HBM, and is laid out to spend as little of it as
+// possible beyond those five instructions per state:
 //
-// Mapping: a 256-thread work-group owns 16 channels of one batch row; lane
-// (wave w, row r = lane / 16, column c = lane % 16) carries the single fp32
-// state n = 4 w + r of channel c and walks the sequence in order, so no
-// carry crosses lanes. 16-channel work-groups give every CU the same share
-// of channels (batch * dim / 16 groups), and one state per lane gives four
-// or five resident wavefronts per SIMD to hide the exp2 -> FMA chain.
+// Mapping: a 256-thread work-group owns 16 channels of one batch row; wave w
+// owns channels 4 w .. 4 w + 3 with all their states: lane (row q = lane /
+// 16, column n = lane % 16) carries the fp32 state n of channel 4 w + q and
+// walks the sequence in order, so no carry crosses lanes. 16-channel
+// work-groups give every CU the same share of channels (batch * dim / 16
+// groups) and one state per lane gives five resident wavefronts per SIMD at
+// config 4 to hide the exp2 -> FMA chain.
 //
 // Per 32-step chunk:
-//   stage  each thread loads 2 steps of u / delta_raw / z of one channel
-//          (64-byte row segments per wave) and B / C of one state, computes
-//          (delta, delta*u) and (B, C) into LDS, and keeps (D*u, silu(z))
-//          in registers for its own outputs; the next chunk's loads are
-//          issued before the recurrence so their latency is hidden.
-//   scan   lanes read (delta, delta*u) of their channel and (B, C) of their
-//          state with 16-byte LDS reads covering two steps (broadcast
-//          across the lanes that share them) and keep C_n x_n per step.
-//   reduce the 16-state sum is a transposed butterfly: v_permlane32_swap
-//          then v_permlane16_swap each exchange one register pair and add,
-//          leaving every lane with the 4-state sum of 8 of the 32 steps;
-//          the four waves' sums meet in LDS.
-//   store  each thread adds the four wave sums for its two steps, applies
-//          D*u and the gate and stores two bf16 outputs.
+//   stage  lane (q, j) loads u, delta_raw and z of its channel at steps j
+//          and j + 16, and keeps (delta, delta*u) for the scan and D*u and
+//          silu(z) for the two outputs it forms itself; B and C of one state
+//          and two steps go to LDS, double-buffered by chunk parity, so one
+//          barrier per chunk suffices. The next chunk's loads are issued
+//          before the scan and first waited for by the next stage.
+//   scan   in two halves of 16 steps: step j's (delta, delta*u) comes from
+//          lane j of the row by DPP row broadcast inside the two multiplies
+//          that use it (v_mul_f32_dpp row_newbcast: no extra instruction),
+//          and after each step the lane writes x to its wave's LDS rows;
+//   output lane (q, j) then forms y of its channel at step 16 h + j as
+//          sum_n C_n x_n with 16 FMAs over four 16-byte reads of the states
+//          and four of C, applies D*u and the gate and stores one bf16.
+// Every exchange of states stays inside the wave that wrote them (a wave's
+// LDS operations execute in order), so the scan and the output need no
+// barrier between them, and the output term costs one FMA per state where
+// a cross-lane reduction of C_n x_n costs a multiply plus exchanges.
+//
+// Addressing: u, delta_raw, z, y, B and C go through buffer resources. A
+// lane's offset is fixed for the launch; each chunk's resources start at
+// its first step and end with the channel block (B, C: the batch row), in
+// scalar registers, so the per-chunk address work is scalar and the
+// hardware range check reads 0 for a load past the end of the block (the
+// sequence's last chunk), whose value goes nowhere: such steps feed no
+// stored output and the last chunk's end state is never read.
 //
 // Sequence-parallel path. When batch * dim / 16 work-groups cannot fill the
 // GPU (few channels, long sequences), the sequence is cut into nch chunks of
@@ -76,8 +88,8 @@ struct ScanArgs {
   int32_t T, nch;  // chunk length and count (1 chunk of L: the single pass)
 };
 
-// the single pass, and the state and output passes of the chunked path
-enum ScanMode { kScanFull = 0, kScanState = 1, kScanOutput = 2 };
+// the output kernel as the single pass, and as the chunked path's output pass
+enum ScanMode { kScanFull = 0, kScanOutput = 1 };
 
 // chunk k of channel d of batch row b: its y segment as fp32 scratch
 // (x[16], then S)
@@ -88,15 +100,6 @@ __device__ inline float *chunk_scratch(const ScanArgs &a, int b, int d, int k) {
 __device__ inline float lo_bf16(uint32_t p) { return __uint_as_float(p << 16); }
 __device__ inline float hi_bf16(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
 
-// two consecutive bf16 elements of a row as packed bits; t is even and
-// elements at or beyond L read as zero
-__device__ inline uint32_t load_pair(const uint16_t *row, int t, int L, bool vec) {
-  if (vec && t + 1 < L) return *(const uint32_t *)(row + t);
-  uint32_t lo = t < L ? row[t] : 0u;
-  uint32_t hi = t + 1 < L ? row[t + 1] : 0u;
-  return lo | (hi << 16);
-}
-
 __device__ inline float softplus_fast(float v) {
   // log(1 + e^v) = ln2 * log2(1 + 2^(v log2 e)); torch returns v above 20
   return v > 20.0f ? v : 0.69314718055994531f * __builtin_amdgcn_logf(1.0f + fast_exp2(v * kLog2e));
@@ -106,54 +109,39 @@ __device__ inline float silu_fast(float z) {
   return z * __builtin_amdgcn_rcpf(1.0f + fast_exp2(-z * kLog2e));
 }
 
-// (lane, lane ^ 32) exchange: returns a_lo + a_hi in the low half and
-// b_lo + b_hi in the high half
-__device__ inline float fold32(float a, float b) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-// row pairs (0,1) and (2,3): returns a summed over the pair in even rows
-// and b summed over the pair in odd rows
-__device__ inline float fold16(float a, float b) {
-  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-template <int MODE>
-__global__ __launch_bounds__(NT) void selective_scan_fwd(ScanArgs a) {
-  // (delta, delta*u) and (B, C) for two steps per float4; one float4 of
-  // padding per row keeps the 16 rows read together in distinct banks
+// The state pass of the chunked path: the recurrence alone, from x = 0, over
+// every chunk but the last; leaves the chunk's end state and delta sum at
+// the start of its own y segment.
+__global__ __launch_bounds__(NT) void selective_scan_state(ScanArgs a) {
+  // (delta, delta*u) for two steps per float4, and B of one state for two
+  // steps; one float4 of padding per row keeps the 16 rows read together in
+  // distinct banks
   __shared__ float4 pre[SCH][TP + 1];
-  __shared__ float4 bcs[ST][TP + 1];
-  // per-wave 4-state sums, [wave][step][channel], padded rows
-  __shared__ float part[4][TT][SCH + 1];
+  __shared__ float2 bsh[ST][TP + 2];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = tid >> 6;
   const int nblk = (a.Dm + SCH - 1) / SCH;
-  // work-group -> (batch row, channel block, chunk); the state pass has no
-  // work-group for the last chunk, whose end state nothing reads
-  const int nwch = MODE == kScanState ? a.nch - 1 : a.nch;
+  // work-group -> (batch row, channel block, chunk); no work-group for the
+  // last chunk, whose end state nothing reads
+  const int nwch = a.nch - 1;
   const int kc = (int)(blockIdx.x % (unsigned)nwch);
   const int grp = (int)(blockIdx.x / (unsigned)nwch);
   const int b = grp / nblk;
   const int d0 = (grp % nblk) * SCH;
   const int tb = kc * a.T;
-  const int te = kc == a.nch - 1 ? a.L : tb + a.T;
+  const int te = tb + a.T;
 
   // scan identity: channel c, state n
   const int c = lane & 15, r = lane >> 4;
   const int n = 4 * w + r;
   const bool cok = d0 + c < a.Dm;
   const float A2 = cok ? a.A[(int64_t)(d0 + c) * ST + n] * kLog2e : 0.0f;
-  // the output pass starts from the carried state the carry pass left in
-  // this chunk's segment (read here, before any store overwrites it)
-  float x = (MODE == kScanOutput && cok) ? chunk_scratch(a, b, d0 + c, kc)[n] : 0.0f;
-  float dsum = 0.0f;  // state pass: this thread's share of the chunk's delta sum
+  float x = 0.0f;
+  float dsum = 0.0f;  // this thread's share of the chunk's delta sum
 
-  // stage / store identity: channel sc, steps 2 sp and 2 sp + 1 of a chunk;
-  // B / C identity: state tid / 16, same step pair
+  // stage identity: channel sc, steps 2 sp and 2 sp + 1 of a chunk; B
+  // identity: state tid / 16, same step pair
   const int sc = tid / TP, sp = tid % TP;
   const int sd = d0 + sc;
   const bool sok = sd < a.Dm;
@@ -161,132 +149,231 @@ __global__ __launch_bounds__(NT) void selective_scan_fwd(ScanArgs a) {
   const int64_t srow = ((int64_t)b * a.Dm + (sok ? sd : 0)) * a.L;
   const int64_t bcrow = ((int64_t)b * ST + bn) * a.L;
   const float bias = (sok && a.bias) ? a.bias[sd] : 0.0f;
-  const float Dd = (sok && a.D) ? a.D[sd] : 0.0f;
-  const bool vec = a.vec != 0;
 
-  // the reduced sums a lane holds after the butterfly are for steps
-  // 4 m + rs, m = 0..7, with rs = 2 (r & 1) + (r >> 1)
-  const int rs = 2 * (r & 1) + (r >> 1);
-
-  uint32_t pu = 0, pdr = 0, pz = 0, pB = 0, pC = 0;
+  // a non-last chunk lies inside the sequence and the path needs even L
+  // and 4-byte aligned rows, so every step pair is one dword
+  uint32_t pu = 0, pdr = 0, pB = 0;
   auto fetch = [&](int t0) {
     const int t = t0 + 2 * sp;
-    if (vec && t0 + TT <= a.L) {  // whole chunk in range: one dword per row
-      if (sok) {
-        pu = *(const uint32_t *)(a.u + srow + t);
-        pdr = *(const uint32_t *)(a.dr + srow + t);
-        if (MODE != kScanState && a.z) pz = *(const uint32_t *)(a.z + srow + t);
-      }
-      pB = *(const uint32_t *)(a.Bm + bcrow + t);
-      if (MODE != kScanState) pC = *(const uint32_t *)(a.Cm + bcrow + t);
-    } else {
-      if (sok) {
-        pu = load_pair(a.u + srow, t, a.L, vec);
-        pdr = load_pair(a.dr + srow, t, a.L, vec);
-        pz = (MODE != kScanState && a.z) ? load_pair(a.z + srow, t, a.L, vec) : 0u;
-      }
-      pB = load_pair(a.Bm + bcrow, t, a.L, vec);
-      if (MODE != kScanState) pC = load_pair(a.Cm + bcrow, t, a.L, vec);
+    if (sok) {
+      pu = *(const uint32_t *)(a.u + srow + t);
+      pdr = *(const uint32_t *)(a.dr + srow + t);
     }
+    pB = *(const uint32_t *)(a.Bm + bcrow + t);
   };
 
   fetch(tb);
   for (int t0 = tb; t0 < te; t0 += TT) {
-    // ---- stage
-    float du2[2], gate[2];
     {
       const float uu[2] = {lo_bf16(pu), hi_bf16(pu)};
       const float dl[2] = {lo_bf16(pdr), hi_bf16(pdr)};
-      const float zz[2] = {lo_bf16(pz), hi_bf16(pz)};
       float4 pv;
       float *pf = reinterpret_cast<float *>(&pv);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const float v = dl[i] + bias;
-        // steps past the end carry delta = 0 and delta*u = 0 (x unchanged)
-        const bool in = t0 + 2 * sp + i < a.L;
-        const float delta = in ? (a.softplus ? softplus_fast(v) : v) : 0.0f;
+        const float delta = a.softplus ? softplus_fast(v) : v;
         pf[2 * i] = delta;
         pf[2 * i + 1] = delta * uu[i];
-        if constexpr (MODE == kScanState) {
-          dsum += delta;
-        } else {
-          du2[i] = Dd * uu[i];
-          gate[i] = a.z ? silu_fast(zz[i]) : 1.0f;
-        }
+        dsum += delta;
       }
       pre[sc][sp] = pv;
-      bcs[bn][sp] = make_float4(lo_bf16(pB), lo_bf16(pC), hi_bf16(pB), hi_bf16(pC));
+      bsh[bn][sp] = make_float2(lo_bf16(pB), hi_bf16(pB));
     }
     if (t0 + TT < te) fetch(t0 + TT);
     __syncthreads();
-
-    if constexpr (MODE == kScanState) {
-      // the recurrence alone
-#pragma unroll
-      for (int j = 0; j < TP; ++j) {
-        const float4 pd = pre[c][j];
-        const float4 q = bcs[n][j];
-        x = fmaf(fast_exp2(pd.x * A2), x, pd.y * q.x);
-        x = fmaf(fast_exp2(pd.z * A2), x, pd.w * q.z);
-      }
-      // pre / bcs are rewritten by the next stage only after every wave is
-      // done with them
-      __syncthreads();
-      continue;
-    }
-
-    // ---- scan: C_n x_n per step
-    float p[TT];
 #pragma unroll
     for (int j = 0; j < TP; ++j) {
       const float4 pd = pre[c][j];
-      const float4 q = bcs[n][j];
+      const float2 q = bsh[n][j];
       x = fmaf(fast_exp2(pd.x * A2), x, pd.y * q.x);
-      p[2 * j] = q.y * x;
-      x = fmaf(fast_exp2(pd.z * A2), x, pd.w * q.z);
-      p[2 * j + 1] = q.w * x;
+      x = fmaf(fast_exp2(pd.z * A2), x, pd.w * q.y);
     }
-    // ---- reduce over the wave's 4 states (rows): after fold32 lane half h
-    // holds steps 2 k + h, after fold16 row r holds steps 4 m + rs
-    float h1[TP];
+    // pre / bsh are rewritten by the next stage only after every wave is
+    // done with them
+    __syncthreads();
+  }
+  if (cok) chunk_scratch(a, b, d0 + c, kc)[n] = x;
 #pragma unroll
-    for (int k = 0; k < TP; ++k) h1[k] = fold32(p[2 * k], p[2 * k + 1]);
+  for (int off = 1; off < TP; off <<= 1) dsum += __shfl_xor(dsum, off, 64);
+  if (sok && sp == 0) chunk_scratch(a, b, sd, kc)[ST] = dsum;
+}
+
+// Cross-lane exchange through LDS inside one wave: the wave's LDS
+// operations execute in order, so only the compiler must keep the accesses
+// on either side of this point in program order.
+__device__ inline void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Lane J of each 16-lane row, broadcast to the whole row (DPP row_newbcast);
+// folded into the VOP2 that consumes it
+template <int J>
+__device__ inline float row_bcast(float v) {
+  static_assert(J >= 0 && J < 16, "row lane");
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + J, 0xf, 0xf, false));
+}
+
+// LDS rows of the output kernel: a wave's states of one step (a step's 64
+// writes fill 64 consecutive banks; the output's 16-byte reads of 16 steps
+// measure two LDS passes where one is the minimum, and a channel-major
+// layout that reads in one pass measured no faster), C of one step, B of one
+// state
+constexpr int XR = 4 * ST + 4;  // floats per xs row
+constexpr int CR = ST + 4;      // floats per C row
+constexpr int BR = TT + 4;      // floats per B row
+
+// a pointer the same for every lane of the work-group, read from the first
+// lane so that it and what is derived from it stay in scalar registers
+template <class T>
+__device__ inline T *uniform_ptr(T *p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  return reinterpret_cast<T *>(((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32)) << 32) |
+                               (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v));
+}
+
+// buffer resource over [base, base + bytes) (base and bytes uniform): loads
+// at or past the end read 0, stores there are dropped
+__device__ inline __amdgpu_buffer_rsrc_t byte_range(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+// The single pass (kScanFull), and the output pass of the chunked path.
+template <int MODE>
+__global__ __launch_bounds__(NT) void selective_scan_out(ScanArgs a) {
+  static_assert(MODE == kScanFull || MODE == kScanOutput, "output kernel modes");
+  __shared__ __attribute__((aligned(16))) float xs[4][TT / 2][XR];    // [wave][step][lane]
+  __shared__ __attribute__((aligned(16))) float bq[2][ST][BR];        // B [parity][state][step]
+  __shared__ __attribute__((aligned(16))) float cs[2][TT][CR];        // C [parity][step][state]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = tid >> 6;
+  const int nblk = (a.Dm + SCH - 1) / SCH;
+  // work-group -> (batch row, channel block, chunk)
+  // (the divisions run on the vector unit: their results are taken back to
+  // scalar registers so that every address derived from them stays scalar)
+  const int kc = __builtin_amdgcn_readfirstlane((int)(blockIdx.x % (unsigned)a.nch));
+  const int grp = (int)(blockIdx.x / (unsigned)a.nch);
+  const int b = __builtin_amdgcn_readfirstlane(grp / nblk);
+  const int d0 = __builtin_amdgcn_readfirstlane((grp % nblk) * SCH);
+  const int tb = kc * a.T;
+  const int te = kc == a.nch - 1 ? a.L : tb + a.T;
+
+  const int q = lane >> 4, n = lane & 15;
+  const int ch = d0 + 4 * w + q;  // this lane's channel
+  const bool cok = ch < a.Dm;
+  const float A2 = cok ? a.A[(int64_t)ch * ST + n] * kLog2e : 0.0f;
+  // the output pass starts from the carried state the carry pass left in
+  // this chunk's segment; every thread reads it before the first barrier,
+  // and the first store of the work-group follows that barrier
+  float x = (MODE == kScanOutput && cok) ? chunk_scratch(a, b, ch, kc)[n] : 0.0f;
+  const float bias = (cok && a.bias) ? a.bias[ch] : 0.0f;
+  const float Dd = (cok && a.D) ? a.D[ch] : 0.0f;
+  // B / C identity: state bn, steps 2 sp and 2 sp + 1
+  const int bn = tid >> 4, sp = tid & 15;
+
+  // rows of this channel block (u, delta_raw, z, y) and of this batch row
+  // (B, C); lanes past the last channel read the block's first row (their
+  // states are never stored)
+  const int64_t blk = ((int64_t)b * a.Dm + d0) * a.L, bcb = (int64_t)b * ST * a.L;
+  const uint32_t rbytes = (uint32_t)(min(SCH, a.Dm - d0) * 2 * a.L);
+  const uint32_t bcbytes = (uint32_t)(ST * 2 * a.L);
+  const uint16_t *ub = uniform_ptr(a.u + blk), *drb = uniform_ptr(a.dr + blk);
+  const uint16_t *zb = uniform_ptr((a.z ? a.z : a.u) + blk);  // z absent: reads u, gate 1
+  const uint16_t *Bb = uniform_ptr(a.Bm + bcb), *Cb = uniform_ptr(a.Cm + bcb);
+  const auto ry = byte_range(uniform_ptr(a.y + blk), rbytes);
+  const uint32_t vo = (uint32_t)(((cok ? 4 * w + q : 0) * a.L + n) * 2);
+  const uint32_t vbc = (uint32_t)((bn * a.L + 2 * sp) * 2);
+  uint32_t fu[2], fdr[2], fz[2], fB[2], fC[2];
+  auto fetch = [&](int t0) {
+    const auto ru = byte_range(ub + t0, rbytes - 2 * t0);
+    const auto rdr = byte_range(drb + t0, rbytes - 2 * t0);
+    const auto rz = byte_range(zb + t0, rbytes - 2 * t0);
+    const auto rB = byte_range(Bb + t0, bcbytes - 2 * t0);
+    const auto rC = byte_range(Cb + t0, bcbytes - 2 * t0);
 #pragma unroll
-    for (int m = 0; m < TT / 4; ++m) {
-      const float s = fold16(h1[2 * m], h1[2 * m + 1]);
-      part[w][4 * m + rs][c] = s;
+    for (int i = 0; i < 2; ++i) {
+      fu[i] = __builtin_amdgcn_raw_buffer_load_b16(ru, vo + 32 * i, 0, 0);
+      fdr[i] = __builtin_amdgcn_raw_buffer_load_b16(rdr, vo + 32 * i, 0, 0);
+      fz[i] = __builtin_amdgcn_raw_buffer_load_b16(rz, vo + 32 * i, 0, 0);
+      fB[i] = __builtin_amdgcn_raw_buffer_load_b16(rB, vbc + 2 * i, 0, 0);
+      fC[i] = __builtin_amdgcn_raw_buffer_load_b16(rC, vbc + 2 * i, 0, 0);
     }
+  };
+
+  float *xw = &xs[w][0][lane];            // this lane's state at step 0
+  const float *xr = &xs[w][n][16 * q];    // row of the output at step n
+
+  fetch(tb);
+  for (int t0 = tb, par = 0; t0 < te; t0 += TT, par ^= 1) {
+    // ---- stage
+    // (delta, delta*u) of steps n and n + 16 of this row's channel: the
+    // scan takes step j's from lane j of the row
+    float du[2], gate[2], dl[2], dlu[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float uu = __uint_as_float(fu[i] << 16);
+      const float v = __uint_as_float(fdr[i] << 16) + bias;
+      // steps past the end carry delta = 0 and delta*u = 0 (x unchanged)
+      const float delta = t0 + n + 16 * i < a.L ? (a.softplus ? softplus_fast(v) : v) : 0.0f;
+      dl[i] = delta;
+      dlu[i] = delta * uu;
+      du[i] = Dd * uu;
+      gate[i] = a.z ? silu_fast(__uint_as_float(fz[i] << 16)) : 1.0f;
+    }
+    *(float2 *)&bq[par][bn][2 * sp] =
+        make_float2(__uint_as_float(fB[0] << 16), __uint_as_float(fB[1] << 16));
+    cs[par][2 * sp][bn] = __uint_as_float(fC[0] << 16);
+    cs[par][2 * sp + 1][bn] = __uint_as_float(fC[1] << 16);
+    if (t0 + TT < te) fetch(t0 + TT);
+    // B / C of this chunk are visible to every wave; cs[par] and bq[par]
+    // are next written two chunks on, behind the next chunk's barrier,
+    // which every wave reaches after its reads of this chunk
     __syncthreads();
 
-    // ---- store
-    if (sok) {
-      float yv[2];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int t = 2 * sp + i;
-        const float acc = part[0][t][sc] + part[1][t][sc] + part[2][t][sc] + part[3][t][sc];
-        yv[i] = (acc + du2[i]) * gate[i];
+    for (int h = 0; h < 2; ++h) {
+      // ---- scan: steps 16 h .. 16 h + 15
+      const float dlh = dl[h], dluh = dlu[h];
+      float4 bv;
+      static_for<16>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        if constexpr (j % 4 == 0) bv = *(const float4 *)&bq[par][n][16 * h + j];
+        const float bj = j % 4 == 0 ? bv.x : j % 4 == 1 ? bv.y : j % 4 == 2 ? bv.z : bv.w;
+        x = fmaf(fast_exp2(row_bcast<j>(dlh) * A2), x, row_bcast<j>(dluh) * bj);
+        xw[j * XR] = x;
+      });
+      wave_lds_sync();
+      // ---- output: this lane's channel at step 16 h + n
+      {
+        const float *cr = &cs[par][16 * h + n][0];
+        float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k += 2) {
+          const float4 x0 = *(const float4 *)(xr + 4 * k);
+          const float4 c0 = *(const float4 *)(cr + 4 * k);
+          const float4 x1 = *(const float4 *)(xr + 4 * k + 4);
+          const float4 c1 = *(const float4 *)(cr + 4 * k + 4);
+          acc0 = fmaf(c0.x, x0.x, acc0);
+          acc1 = fmaf(c1.x, x1.x, acc1);
+          acc0 = fmaf(c0.y, x0.y, acc0);
+          acc1 = fmaf(c1.y, x1.y, acc1);
+          acc0 = fmaf(c0.z, x0.z, acc0);
+          acc1 = fmaf(c1.z, x1.z, acc1);
+          acc0 = fmaf(c0.w, x0.w, acc0);
+          acc1 = fmaf(c1.w, x1.w, acc1);
+        }
+        const int t = t0 + 16 * h + n;
+        if (cok && t < a.L)
+          __builtin_amdgcn_raw_buffer_store_b16(
+              Bf16Tag::from_f32((acc0 + acc1 + du[h]) * gate[h]), ry, vo + 32 * h, 2 * t0, 0);
       }
-      const int t = t0 + 2 * sp;
-      uint16_t *yrow = a.y + srow;
-      if (vec && t + 1 < a.L) {
-        *(uint32_t *)(yrow + t) = Bf16Tag::pack2(yv[0], yv[1]);
-      } else {
-        if (t < a.L) yrow[t] = Bf16Tag::from_f32(yv[0]);
-        if (t + 1 < a.L) yrow[t + 1] = Bf16Tag::from_f32(yv[1]);
-      }
+      // the next half (or chunk) rewrites xs only after these reads
+      wave_lds_sync();
     }
-    // pre / bcs are rewritten by the next stage only after every wave has
-    // passed this chunk's second barrier, and part only after the next
-    // chunk's first barrier, which every wave reaches after its stores
-  }
-  if constexpr (MODE == kScanState) {
-    // the chunk's end state and delta sum, at the start of its own segment
-    if (cok) chunk_scratch(a, b, d0 + c, kc)[n] = x;
-#pragma unroll
-    for (int off = 1; off < TP; off <<= 1) dsum += __shfl_xor(dsum, off, 64);
-    if (sok && sp == 0) chunk_scratch(a, b, sd, kc)[ST] = dsum;
   }
 }
 
@@ -328,6 +415,7 @@ __global__ __launch_bounds__(256) void selective_scan_carry(ScanArgs a, int32_t 
 // 64; the last chunk takes the remainder (T .. 2T - 1 steps). nch = 1: the
 // single pass. The chunked path needs the 4-byte pair access (even L).
 constexpr int64_t kScanFillGroups = 1024, kScanTargetGroups = 1280, kScanMinChunk = 64;
+constexpr int64_t kScanMaxSeq = (int64_t)1 << 26;  // 16 rows x 2 bytes x 2^26 = 2^31
 
 void scan_chunking(int64_t batch, int64_t dim, int64_t L, bool vec, int32_t *T, int32_t *nch) {
   const int64_t groups = (dim + SCH - 1) / SCH * batch;
@@ -350,7 +438,13 @@ bool scan_supported(const ScanLaunch &a, const char **why) {
     *why = "selective scan supports d_state 16";
     return false;
   }
-  if (a.seq_len > (int64_t)1 << 30 || a.dim > (int64_t)1 << 30 ||
+  // the output kernel addresses a channel block (16 rows) and a batch row of
+  // B / C (16 rows) through 32-bit byte offsets
+  if (a.seq_len >= kScanMaxSeq) {
+    *why = "selective scan supports seq_len below 2^26";
+    return false;
+  }
+  if (a.dim > (int64_t)1 << 30 ||
       a.batch * ((a.dim + SCH - 1) / SCH) > (((int64_t)1 << 31) - 1)) {
     *why = "selective scan shape too large for one launch";
     return false;
@@ -378,15 +472,15 @@ hipError_t launch_selective_scan(const ScanLaunch &L, hipStream_t s) {
   const int64_t groups = (L.dim + SCH - 1) / SCH * L.batch;
   scan_chunking(L.batch, L.dim, L.seq_len, a.vec != 0, &a.T, &a.nch);
   if (a.nch <= 1) {
-    hipLaunchKernelGGL(selective_scan_fwd<kScanFull>, dim3((unsigned)groups), dim3(NT), 0, s, a);
+    hipLaunchKernelGGL(selective_scan_out<kScanFull>, dim3((unsigned)groups), dim3(NT), 0, s, a);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL(selective_scan_fwd<kScanState>, dim3((unsigned)(groups * (a.nch - 1))),
-                     dim3(NT), 0, s, a);
+  hipLaunchKernelGGL(selective_scan_state, dim3((unsigned)(groups * (a.nch - 1))), dim3(NT), 0,
+                     s, a);
   const int64_t lanes = L.batch * L.dim * ST;
   hipLaunchKernelGGL(selective_scan_carry, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0,
                      s, a, (int32_t)lanes);
-  hipLaunchKernelGGL(selective_scan_fwd<kScanOutput>, dim3((unsigned)(groups * a.nch)), dim3(NT),
+  hipLaunchKernelGGL(selective_scan_out<kScanOutput>, dim3((unsigned)(groups * a.nch)), dim3(NT),
                      0, s, a);
   return hipGetLastError();
 }

@@ -374,6 +374,13 @@ def test_quantize_and_scan_validation(lib):
     assert s(ctypes.byref(n8), *([FAKE] * 9), None) == _abi.ERR_UNSUPPORTED
     assert s(ctypes.byref(d), FAKE, FAKE, FAKE, FAKE, None, FAKE, FAKE, FAKE, FAKE,
              None) == _abi.ERR_INVALID_ARGUMENT  # C missing
+    # the output kernel's 32-bit offsets span 16 rows of a sequence: below 2^26 steps
+    long_seq = _abi.ScanDesc(1, 16, 1 << 26, 16, _abi.DTYPE_BF16, 1)
+    assert s(ctypes.byref(long_seq), *([FAKE] * 9), None) == _abi.ERR_UNSUPPORTED
+    assert b"seq_len below 2^26" in lib.neptune_last_error()
+    if lib.neptune_device_count() == 0:
+        just_under = _abi.ScanDesc(1, 16, (1 << 26) - 2, 16, _abi.DTYPE_BF16, 1)
+        assert s(ctypes.byref(just_under), *([FAKE] * 9), None) == _abi.ERR_NO_DEVICE
 
 
 def test_no_device_path(lib):
