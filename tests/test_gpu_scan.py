@@ -145,3 +145,32 @@ def test_scan_chunked_repeated_call_is_identical(ops):
     y2 = ops.selective_scan(*ins)
     torch.cuda.synchronize()
     assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+
+
+@pytest.mark.parametrize("softplus", [True, False])
+@pytest.mark.parametrize("b,d,L", [(2, 40, 301), (1, 32, 4096)])
+def test_scan_softplus_branches(ops, b, d, L, softplus):
+    """Softplus on: delta_raw + bias spread over [-30, 30], so both the
+    threshold branch (delta = the input above 20) and the exp / log branch
+    run. Softplus off: a positive delta_raw + bias feeds delta directly. The
+    first shape takes the single pass, the second the chunked path (whose
+    state pass computes delta on its own)."""
+    assert _chunked(b, d, L) == (L == 4096)
+    _log(f"case: scan softplus={softplus} b={b} d={d} L={L}")
+    u, dr, A, Bm, Cm, D, z, bias = scan_inputs(b, d, L, seed=700 + L)
+    g = torch.Generator().manual_seed(710 + L)
+    if softplus:
+        dr = (torch.rand((b, d, L), generator=g) * 60.0 - 30.0).to(torch.bfloat16)
+    else:
+        dr = (torch.rand((b, d, L), generator=g) * 0.5 + 0.01).to(torch.bfloat16)
+        bias = torch.rand((d,), generator=g) * 0.1
+    y = ops.selective_scan(u.cuda(), dr.cuda(), A.cuda(), Bm.cuda(), Cm.cuda(), D.cuda(),
+                           z.cuda(), bias.cuda(), delta_softplus=softplus)
+    torch.cuda.synchronize()
+    ref_bits, _ = oracle.selective_scan(bits(u), bits(dr), A.numpy(), bits(Bm), bits(Cm),
+                                        D.numpy(), bits(z), bias.numpy(), softplus=softplus)
+    ref = oracle.decode(ref_bits, oracle.BF16).astype(np.float64)
+    got = to_f32(y).astype(np.float64)
+    assert np.isfinite(got).all()
+    bad = np.abs(got - ref) > 2e-2 * np.maximum(1.0, np.abs(ref))
+    assert not bad.any(), (np.argwhere(bad)[:5], np.abs(got - ref).max())
