@@ -13,7 +13,11 @@ checks the result against the CPU oracle at the contract's tolerances:
   32, 64 and 128 tokens;
 * paged decode (neptune_decode_paged, neptune_decode_paged_fp8): page sizes
   32-256, both pool layouts, bf16 and fp8 pools, ragged lengths including
-  empty sequences.
+  empty sequences;
+* selective scan (neptune_selective_scan_fwd): batch 1-3, ragged channel
+  counts, lengths 1-1500 (odd ones take the single pass, even ones of two
+  64-step chunks or more the chunked path when the channels leave the GPU
+  unfilled), with or without z, D and delta_bias, softplus on or off.
 """
 
 import numpy as np
@@ -204,3 +208,44 @@ def test_paged_decode_sweep(ops, i):
     ref = oracle.decode(ro, oracle.BF16)
     assert max_abs(to_f32(o), ref) <= (TOL_FP8_ABS if fp8 else TOL_BF16_ABS)
     _lse_close(to_f32(lse), rl)
+
+
+def _scan_case(i):
+    rng = np.random.default_rng(4000 + i)
+    return dict(b=int(rng.integers(1, 4)), d=int(rng.integers(1, 200)),
+                L=int(rng.integers(1, 1500)), gate=bool(rng.integers(0, 2)),
+                with_d=bool(rng.integers(0, 2)), bias=bool(rng.integers(0, 2)),
+                softplus=bool(rng.integers(0, 4)), seed=4000 + i)
+
+
+@pytest.mark.parametrize("i", range(60))
+def test_scan_sweep(ops, i):
+    c = _scan_case(i)
+    _log(f"case: scan sweep {c}")
+    b, d, L, n = c["b"], c["d"], c["L"], 16
+    u, z = randn((b, d, L), seed=c["seed"]), randn((b, d, L), seed=c["seed"] + 1)
+    Bm, Cm = randn((b, n, L), seed=c["seed"] + 2), randn((b, n, L), seed=c["seed"] + 3)
+    A = -torch.exp(randn((d, n), seed=c["seed"] + 4, dtype=torch.float32))
+    D = randn((d,), seed=c["seed"] + 5, dtype=torch.float32) if c["with_d"] else None
+    g = torch.Generator().manual_seed(c["seed"] + 6)
+    if c["softplus"]:
+        dr = randn((b, d, L), seed=c["seed"] + 7)
+        bias = randn((d,), seed=c["seed"] + 8, dtype=torch.float32) if c["bias"] else None
+    else:  # delta = delta_raw + bias directly: keep it positive
+        dr = (torch.rand((b, d, L), generator=g) * 0.5 + 0.01).to(torch.bfloat16)
+        bias = torch.rand((d,), generator=g) * 0.1 if c["bias"] else None
+    y = ops.selective_scan(u.cuda(), dr.cuda(), A.cuda(), Bm.cuda(), Cm.cuda(),
+                           None if D is None else D.cuda(), z.cuda() if c["gate"] else None,
+                           None if bias is None else bias.cuda(),
+                           delta_softplus=c["softplus"])
+    torch.cuda.synchronize()
+    ref_bits, _ = oracle.selective_scan(bits(u), bits(dr), A.numpy(), bits(Bm), bits(Cm),
+                                        None if D is None else D.numpy(),
+                                        bits(z) if c["gate"] else None,
+                                        None if bias is None else bias.numpy(),
+                                        softplus=c["softplus"])
+    ref = oracle.decode(ref_bits, oracle.BF16).astype(np.float64)
+    got = to_f32(y).astype(np.float64)
+    assert np.isfinite(got).all()
+    bad = np.abs(got - ref) > 2e-2 * np.maximum(1.0, np.abs(ref))
+    assert not bad.any(), (np.argwhere(bad)[:5], np.abs(got - ref).max())
