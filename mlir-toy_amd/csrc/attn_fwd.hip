@@ -242,6 +242,25 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_mfma(AttnArgs a) {
   }
 }
 
+// sum / max over the 16 lanes of a row (DPP row rotations, no LDS): every
+// lane of the row gets the result
+template <int R>
+__device__ inline float row_ror(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + R, 0xf, 0xf, false));
+}
+__device__ inline float row_sum16(float v) {
+  v += row_ror<8>(v);
+  v += row_ror<4>(v);
+  v += row_ror<2>(v);
+  return v + row_ror<1>(v);
+}
+__device__ inline float row_max16(float v) {
+  v = fmaxf(v, row_ror<8>(v));
+  v = fmaxf(v, row_ror<4>(v));
+  v = fmaxf(v, row_ror<2>(v));
+  return fmaxf(v, row_ror<1>(v));
+}
+
 // fp32 path (config 1 and any F32 request): a 256-thread work-group per 16
 // query rows, 16 lanes per row. K/V blocks of 64 keys are staged in LDS;
 // lane k of a row takes keys k, k + 16, k + 32, k + 48 of each block and
@@ -271,10 +290,13 @@ __global__ __launch_bounds__(F32_NT) void attn_fwd_f32(AttnArgs a) {
   const float *vp = (const float *)a.v + b * a.vs0 + hk * a.vs1;
   const int row = qb * F32_BM + rl;
 
+  // rows past the end read the last row (never stored), so no load is
+  // guarded and all of them issue before the first is waited for
+  const int rowc = min(row, a.Sq - 1);
   float q[D], acc[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
-    q[d] = row < a.Sq ? qp[row * a.qs2 + d] : 0.0f;
+    q[d] = qp[rowc * a.qs2 + d];
     acc[d] = 0.0f;
   }
   float m = kNegFltMax, lsum = 0.0f;
@@ -288,10 +310,24 @@ __global__ __launch_bounds__(F32_NT) void attn_fwd_f32(AttnArgs a) {
   for (int jb = 0; jb < nkb; ++jb) {
     const int key0 = jb * BN;
     __syncthreads();
-    for (int e = t; e < BN * D; e += F32_NT) {
-      const int r = e / D, c = e % D, key = key0 + r;
-      Ks[r][c] = key < a.Sk ? kp[key * a.ks2 + c] : 0.0f;
-      Vs[r][c] = key < a.Sk ? vp[key * a.vs2 + c] : 0.0f;
+    // a fixed trip count, unrolled, so every element's load issues before
+    // the first one is waited for
+    static_assert(BN * D % F32_NT == 0, "whole staging rounds");
+    float kv[BN * D / F32_NT], vv[BN * D / F32_NT];
+#pragma unroll
+    for (int i = 0; i < BN * D / F32_NT; ++i) {
+      const int e = t + i * F32_NT;
+      // keys past the end read the last key: their scores are masked to
+      // -inf, so their p is 0
+      const int r = e / D, c = e % D, key = min(key0 + r, a.Sk - 1);
+      kv[i] = kp[key * a.ks2 + c];
+      vv[i] = vp[key * a.vs2 + c];
+    }
+#pragma unroll
+    for (int i = 0; i < BN * D / F32_NT; ++i) {
+      const int e = t + i * F32_NT;
+      Ks[e / D][e % D] = kv[i];
+      Vs[e / D][e % D] = vv[i];
     }
     __syncthreads();
     float s[KPL];
@@ -330,24 +366,22 @@ __global__ __launch_bounds__(F32_NT) void attn_fwd_f32(AttnArgs a) {
   }
   // merge the 16 lane states of the row (lanes rl * 16 .. rl * 16 + 15 of
   // one wave): a lane that saw no visible key has m = -FLT_MAX and l = 0
-  float M = m;
-#pragma unroll
-  for (int off = 1; off < F32_KS; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+  const float M = row_max16(m);
   const float wgt = fast_exp2(m - M);
-  float ltot = lsum * wgt;
+  const float ltot = row_sum16(lsum * wgt);
 #pragma unroll
-  for (int off = 1; off < F32_KS; off <<= 1) ltot += __shfl_xor(ltot, off, 64);
-#pragma unroll
-  for (int d = 0; d < D; ++d) {
-    float v = acc[d] * wgt;
-#pragma unroll
-    for (int off = 1; off < F32_KS; off <<= 1) v += __shfl_xor(v, off, 64);
-    acc[d] = v;
-  }
+  for (int d = 0; d < D; ++d) acc[d] = row_sum16(acc[d] * wgt);
   if (row < a.Sq && kl == 0) {
+    // the correctly rounded quotient acc / l (HTile:130-143): q = acc * (1/l)
+    // with the correctly rounded reciprocal, then one residual step
+    // q + fma(-q, l, acc) * (1/l) (Markstein's correction)
+    const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
     float *op = (float *)a.o + b * a.os0 + h * a.os1 + row * a.os2;
 #pragma unroll
-    for (int d = 0; d < D; ++d) op[d] = ltot > 0.0f ? acc[d] / ltot : 0.0f;
+    for (int d = 0; d < D; ++d) {
+      const float q0 = acc[d] * inv;
+      op[d] = __builtin_fmaf(__builtin_fmaf(-q0, ltot, acc[d]), inv, q0);
+    }
     if (a.lse)
       a.lse[((int64_t)b * a.Hq + h) * a.Sq + row] =
           ltot > 0.0f ? (M + log2f(ltot)) * kLn2 : -INFINITY;
