@@ -23,30 +23,49 @@
 //
 // Per 32-step chunk:
 //   stage  lane (q, j) loads u, delta_raw and z of its channel at steps j
-//          and j + 16, and keeps (delta, delta*u) for the scan and D*u and
-//          silu(z) for the two outputs it forms itself; B and C of one state
-//          and two steps go to LDS, double-buffered by chunk parity, so one
-//          barrier per chunk suffices. The next chunk's loads are issued
-//          before the scan and first waited for by the next stage.
-//   scan   in two halves of 16 steps: step j's (delta, delta*u) comes from
-//          lane j of the row by DPP row broadcast inside the two multiplies
-//          that use it (v_mul_f32_dpp row_newbcast: no extra instruction),
-//          and after each step the lane writes x to its wave's LDS rows;
+//          and j + 16, and keeps (delta log2 e, delta u) for the scan and
+//          u ln2 and silu(z) for the two outputs it forms itself; B and C of
+//          one state and two steps go to LDS, double-buffered by chunk
+//          parity, so one barrier per chunk suffices. The next chunk's loads
+//          are issued before the scan and first waited for by the next stage.
+//          Working in log2 units, delta log2 e is one FMA of delta_raw (plus
+//          the softplus, whose exp2 / log2 take it directly), the decay is
+//          2^(delta log2 e * A), and the output's D u is (D log2 e)(u ln2)
+//          inside one FMA.
+//   scan   in two halves of 16 steps: step j's (delta log2 e, delta u) comes
+//          from lane j of the row by DPP row broadcast inside the two
+//          multiplies that use it (v_mul_f32_dpp row_newbcast: no extra
+//          instruction), and after each step the lane writes x to its wave's
+//          LDS rows;
 //   output lane (q, j) then forms y of its channel at step 16 h + j as
 //          sum_n C_n x_n with 16 FMAs over four 16-byte reads of the states
-//          and four of C, applies D*u and the gate and stores one bf16.
+//          and four of C, and applies D*u and the gate; the chunk's two
+//          bf16 outputs per lane are stored in the next chunk.
 // Every exchange of states stays inside the wave that wrote them (a wave's
 // LDS operations execute in order), so the scan and the output need no
 // barrier between them, and the output term costs one FMA per state where
 // a cross-lane reduction of C_n x_n costs a multiply plus exchanges.
 //
+// Memory waits: loads and stores share the vector-memory counter, so a wait
+// for the fetched data also waits for every store issued before it. The
+// chunk loop therefore runs in pairs with two register sets for the loads
+// (the parity, and the LDS offsets it selects, are constants), stores each
+// chunk's outputs after the next chunk's fetch and barrier, unconditionally
+// (a lane without an output stores out of range), and keeps their data
+// registers until the stores are old; its barrier orders LDS only, so the
+// stores stay in flight across it. Each chunk then waits for its own data
+// with the two newest stores still outstanding.
+//
 // Addressing: u, delta_raw, z, y, B and C go through buffer resources. A
 // lane's offset is fixed for the launch; each chunk's resources start at
 // its first step and end with the channel block (B, C: the batch row), in
 // scalar registers, so the per-chunk address work is scalar and the
-// hardware range check reads 0 for a load past the end of the block (the
-// sequence's last chunk), whose value goes nowhere: such steps feed no
-// stored output and the last chunk's end state is never read.
+// hardware range check reads 0 for a load past the end of the block.
+// Steps past the end of the sequence (in its last chunk) are not masked:
+// they read the next row of the block, or 0, and scan on. They come after
+// every real step of the chunk, their states only reach the LDS rows of
+// their own steps, whose outputs are not stored, and the last chunk's end
+// state is never read, so whatever they compute goes nowhere.
 //
 // Sequence-parallel path. When batch * dim / 16 work-groups cannot fill the
 // GPU (few channels, long sequences), the sequence is cut into nch chunks of
@@ -208,6 +227,16 @@ __device__ inline void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Work-group barrier that orders LDS only. A __syncthreads() fence also
+// orders global memory, so it waits for every store issued before it; the
+// output kernel's barriers exchange LDS data only, and its stores may stay
+// in flight across them.
+__device__ inline void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Lane J of each 16-lane row, broadcast to the whole row (DPP row_newbcast);
 // folded into the VOP2 that consumes it
 template <int J>
@@ -241,9 +270,18 @@ __device__ inline __amdgpu_buffer_rsrc_t byte_range(const void *base, uint32_t b
                                            0x00020000);
 }
 
-// The single pass (kScanFull), and the output pass of the chunked path.
-template <int MODE>
-__global__ __launch_bounds__(NT) void selective_scan_out(ScanArgs a) {
+// softplus's linear branch (torch: delta_raw + bias above 20), in log2 units
+constexpr float kSoftplusLinear2 = 20.0f * kLog2e;
+// a byte offset past every output resource (at most 16 rows x 2 x 2^26
+// bytes): a store there is dropped by the range check
+constexpr uint32_t kDropped = 0x80000000u;
+
+// The single pass (kScanFull), and the output pass of the chunked path;
+// SOFTPLUS and GATE (z given) are fixed per launch. Five work-groups per CU
+// (at most 96 VGPRs): what config 4's 1280 work-groups need to run in one
+// round.
+template <int MODE, bool SOFTPLUS, bool GATE>
+__global__ __launch_bounds__(NT, 5) void selective_scan_out(ScanArgs a) {
   static_assert(MODE == kScanFull || MODE == kScanOutput, "output kernel modes");
   __shared__ __attribute__((aligned(16))) float xs[4][TT / 2][XR];    // [wave][step][lane]
   __shared__ __attribute__((aligned(16))) float bq[2][ST][BR];        // B [parity][state][step]
@@ -265,13 +303,15 @@ __global__ __launch_bounds__(NT) void selective_scan_out(ScanArgs a) {
   const int q = lane >> 4, n = lane & 15;
   const int ch = d0 + 4 * w + q;  // this lane's channel
   const bool cok = ch < a.Dm;
-  const float A2 = cok ? a.A[(int64_t)ch * ST + n] * kLog2e : 0.0f;
+  // the decay 2^(delta log2 e * A) takes A as it is
+  const float Ac = cok ? a.A[(int64_t)ch * ST + n] : 0.0f;
   // the output pass starts from the carried state the carry pass left in
-  // this chunk's segment; every thread reads it before the first barrier,
-  // and the first store of the work-group follows that barrier
+  // this chunk's segment; every thread holds it (the load retired, below)
+  // before the first barrier, and the work-group's first store follows that
+  // barrier
   float x = (MODE == kScanOutput && cok) ? chunk_scratch(a, b, ch, kc)[n] : 0.0f;
-  const float bias = (cok && a.bias) ? a.bias[ch] : 0.0f;
-  const float Dd = (cok && a.D) ? a.D[ch] : 0.0f;
+  const float bias2 = (cok && a.bias) ? a.bias[ch] * kLog2e : 0.0f;
+  const float D2 = (cok && a.D) ? a.D[ch] * kLog2e : 0.0f;  // times u ln2: D u
   // B / C identity: state bn, steps 2 sp and 2 sp + 1
   const int bn = tid >> 4, sp = tid & 15;
 
@@ -282,57 +322,87 @@ __global__ __launch_bounds__(NT) void selective_scan_out(ScanArgs a) {
   const uint32_t rbytes = (uint32_t)(min(SCH, a.Dm - d0) * 2 * a.L);
   const uint32_t bcbytes = (uint32_t)(ST * 2 * a.L);
   const uint16_t *ub = uniform_ptr(a.u + blk), *drb = uniform_ptr(a.dr + blk);
-  const uint16_t *zb = uniform_ptr((a.z ? a.z : a.u) + blk);  // z absent: reads u, gate 1
+  const uint16_t *zb = uniform_ptr((GATE ? a.z : a.u) + blk);
   const uint16_t *Bb = uniform_ptr(a.Bm + bcb), *Cb = uniform_ptr(a.Cm + bcb);
   const auto ry = byte_range(uniform_ptr(a.y + blk), rbytes);
   const uint32_t vo = (uint32_t)(((cok ? 4 * w + q : 0) * a.L + n) * 2);
   const uint32_t vbc = (uint32_t)((bn * a.L + 2 * sp) * 2);
-  uint32_t fu[2], fdr[2], fz[2], fB[2], fC[2];
-  auto fetch = [&](int t0) {
-    const auto ru = byte_range(ub + t0, rbytes - 2 * t0);
-    const auto rdr = byte_range(drb + t0, rbytes - 2 * t0);
-    const auto rz = byte_range(zb + t0, rbytes - 2 * t0);
-    const auto rB = byte_range(Bb + t0, bcbytes - 2 * t0);
-    const auto rC = byte_range(Cb + t0, bcbytes - 2 * t0);
+  // Two register sets for the loads: a chunk of parity P stages from set P
+  // and fetches the next chunk into set 1 - P (the chunk loop runs in pairs,
+  // so the parity and every LDS offset derived from it are constants)
+  uint32_t fu[2][2], fdr[2][2], fz[2][2], fB[2][2], fC[2][2];
+  // (issued unconditionally: past the end of the sequence the resources
+  // cover 0 bytes and the loads read 0)
+  auto fetch = [&](auto S, int t0) {
+    constexpr int set = decltype(S)::value;
+    const uint32_t rb = t0 < a.L ? rbytes - 2 * t0 : 0, bcb2 = t0 < a.L ? bcbytes - 2 * t0 : 0;
+    const auto ru = byte_range(ub + t0, rb);
+    const auto rdr = byte_range(drb + t0, rb);
+    const auto rz = byte_range(zb + t0, rb);
+    const auto rB = byte_range(Bb + t0, bcb2);
+    const auto rC = byte_range(Cb + t0, bcb2);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      fu[i] = __builtin_amdgcn_raw_buffer_load_b16(ru, vo + 32 * i, 0, 0);
-      fdr[i] = __builtin_amdgcn_raw_buffer_load_b16(rdr, vo + 32 * i, 0, 0);
-      fz[i] = __builtin_amdgcn_raw_buffer_load_b16(rz, vo + 32 * i, 0, 0);
-      fB[i] = __builtin_amdgcn_raw_buffer_load_b16(rB, vbc + 2 * i, 0, 0);
-      fC[i] = __builtin_amdgcn_raw_buffer_load_b16(rC, vbc + 2 * i, 0, 0);
+      fu[set][i] = __builtin_amdgcn_raw_buffer_load_b16(ru, vo + 32 * i, 0, 0);
+      fdr[set][i] = __builtin_amdgcn_raw_buffer_load_b16(rdr, vo + 32 * i, 0, 0);
+      if constexpr (GATE)
+        fz[set][i] = __builtin_amdgcn_raw_buffer_load_b16(rz, vo + 32 * i, 0, 0);
+      fB[set][i] = __builtin_amdgcn_raw_buffer_load_b16(rB, vbc + 2 * i, 0, 0);
+      fC[set][i] = __builtin_amdgcn_raw_buffer_load_b16(rC, vbc + 2 * i, 0, 0);
     }
   };
 
   float *xw = &xs[w][0][lane];            // this lane's state at step 0
   const float *xr = &xs[w][n][16 * q];    // row of the output at step n
 
-  fetch(tb);
-  for (int t0 = tb, par = 0; t0 < te; t0 += TT, par ^= 1) {
+  // A chunk's two outputs per lane are stored in the next chunk, after its
+  // fetch and barrier: the next wait on the vector-memory counter (shared by
+  // loads and stores) is then a chunk away, so it never waits on a store
+  // issued just before it
+  // The stores are issued by every lane, unconditionally, so that the
+  // compiler counts them exactly: a lane with no output (past the end of
+  // the sequence, or past the last channel) stores past the resource's
+  // range, where the hardware drops it.
+  uint16_t yq[2] = {0, 0};
+  auto store_outputs = [&](int tp) {  // tp: the chunk's first step
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const bool live = cok && n < a.L - tp - 16 * h;
+      __builtin_amdgcn_raw_buffer_store_b16(yq[h], ry, live ? vo + 32 * h + 2 * tp : kDropped, 0, 0);
+    }
+  };
+
+  // the 32-step chunk from t0, of parity P; the first one has no previous
+  // outputs to store
+  auto chunk = [&](auto P, auto FIRST, int t0) {
+    constexpr int par = decltype(P)::value;
     // ---- stage
-    // (delta, delta*u) of steps n and n + 16 of this row's channel: the
-    // scan takes step j's from lane j of the row
-    float du[2], gate[2], dl[2], dlu[2];
+    // (delta log2 e, delta u) of steps n and n + 16 of this row's channel:
+    // the scan takes step j's from lane j of the row
+    float ul[2], gate[2], dl[2], dlu[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const float uu = __uint_as_float(fu[i] << 16);
-      const float v = __uint_as_float(fdr[i] << 16) + bias;
-      // steps past the end carry delta = 0 and delta*u = 0 (x unchanged)
-      const float delta = t0 + n + 16 * i < a.L ? (a.softplus ? softplus_fast(v) : v) : 0.0f;
-      dl[i] = delta;
-      dlu[i] = delta * uu;
-      du[i] = Dd * uu;
-      gate[i] = a.z ? silu_fast(__uint_as_float(fz[i] << 16)) : 1.0f;
+      const float uln2 = __uint_as_float(fu[par][i] << 16) * kLn2;
+      // (delta_raw + bias) log2 e, and delta log2 e = log2(1 + 2^that)
+      // below the linear branch
+      const float v2 = fmaf(__uint_as_float(fdr[par][i] << 16), kLog2e, bias2);
+      const float d2 =
+          SOFTPLUS && !(v2 > kSoftplusLinear2) ? __builtin_amdgcn_logf(1.0f + fast_exp2(v2)) : v2;
+      dl[i] = d2;
+      dlu[i] = d2 * uln2;
+      ul[i] = uln2;
+      gate[i] = GATE ? silu_fast(__uint_as_float(fz[par][i] << 16)) : 1.0f;
     }
     *(float2 *)&bq[par][bn][2 * sp] =
-        make_float2(__uint_as_float(fB[0] << 16), __uint_as_float(fB[1] << 16));
-    cs[par][2 * sp][bn] = __uint_as_float(fC[0] << 16);
-    cs[par][2 * sp + 1][bn] = __uint_as_float(fC[1] << 16);
-    if (t0 + TT < te) fetch(t0 + TT);
+        make_float2(__uint_as_float(fB[par][0] << 16), __uint_as_float(fB[par][1] << 16));
+    cs[par][2 * sp][bn] = __uint_as_float(fC[par][0] << 16);
+    cs[par][2 * sp + 1][bn] = __uint_as_float(fC[par][1] << 16);
+    fetch(std::integral_constant<int, 1 - par>{}, t0 + TT);
     // B / C of this chunk are visible to every wave; cs[par] and bq[par]
     // are next written two chunks on, behind the next chunk's barrier,
     // which every wave reaches after its reads of this chunk
-    __syncthreads();
+    lds_barrier();
+    if constexpr (!decltype(FIRST)::value) store_outputs(t0 - TT);
 
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -343,10 +413,14 @@ __global__ __launch_bounds__(NT) void selective_scan_out(ScanArgs a) {
         constexpr int j = decltype(J)::value;
         if constexpr (j % 4 == 0) bv = *(const float4 *)&bq[par][n][16 * h + j];
         const float bj = j % 4 == 0 ? bv.x : j % 4 == 1 ? bv.y : j % 4 == 2 ? bv.z : bv.w;
-        x = fmaf(fast_exp2(row_bcast<j>(dlh) * A2), x, row_bcast<j>(dluh) * bj);
+        x = fmaf(fast_exp2(row_bcast<j>(dlh) * Ac), x, row_bcast<j>(dluh) * bj);
         xw[j * XR] = x;
       });
       wave_lds_sync();
+      // the previous chunk's outputs, stored after this chunk's barrier,
+      // keep their registers until here: writing over a store's data
+      // register waits for that store
+      if (h == 0) asm volatile("" ::"v"(yq[0]), "v"(yq[1]));
       // ---- output: this lane's channel at step 16 h + n
       {
         const float *cr = &cs[par][16 * h + n][0];
@@ -366,15 +440,27 @@ __global__ __launch_bounds__(NT) void selective_scan_out(ScanArgs a) {
           acc0 = fmaf(c0.w, x0.w, acc0);
           acc1 = fmaf(c1.w, x1.w, acc1);
         }
-        const int t = t0 + 16 * h + n;
-        if (cok && t < a.L)
-          __builtin_amdgcn_raw_buffer_store_b16(
-              Bf16Tag::from_f32((acc0 + acc1 + du[h]) * gate[h]), ry, vo + 32 * h, 2 * t0, 0);
+        const float yv = fmaf(D2, ul[h], acc0 + acc1);
+        yq[h] = Bf16Tag::from_f32(GATE ? yv * gate[h] : yv);
+        // formed here, not sunk past the next half's scan with its 32
+        // operands held live (the store is a chunk away)
+        asm volatile("" ::"v"(yq[h]));
       }
       // the next half (or chunk) rewrites xs only after these reads
       wave_lds_sync();
     }
+  };
+
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  fetch(P0{}, tb);
+  if constexpr (MODE == kScanOutput) asm volatile("" ::"v"(x));  // the load of x has retired
+  chunk(P0{}, std::true_type{}, tb);
+  for (int t0 = tb + TT; t0 < te; t0 += 2 * TT) {
+    chunk(P1{}, std::false_type{}, t0);
+    if (t0 + TT < te) chunk(P0{}, std::false_type{}, t0 + TT);
   }
+  store_outputs(tb + (te - tb - 1) / TT * TT);  // the last chunk's
 }
 
 // The carry pass: one lane per (batch row, channel, state) walks the chunks
@@ -471,8 +557,16 @@ hipError_t launch_selective_scan(const ScanLaunch &L, hipStream_t s) {
           al4(L.y) && (!L.z || al4(L.z));
   const int64_t groups = (L.dim + SCH - 1) / SCH * L.batch;
   scan_chunking(L.batch, L.dim, L.seq_len, a.vec != 0, &a.T, &a.nch);
+  const bool sp = L.delta_softplus != 0, gate = L.z != nullptr;
+  // the output kernel for this mode and these options
+  auto out = [&](auto mode, unsigned grid) {
+    constexpr int M = decltype(mode)::value;
+    auto k = sp ? (gate ? selective_scan_out<M, true, true> : selective_scan_out<M, true, false>)
+                : (gate ? selective_scan_out<M, false, true> : selective_scan_out<M, false, false>);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(NT), 0, s, a);
+  };
   if (a.nch <= 1) {
-    hipLaunchKernelGGL(selective_scan_out<kScanFull>, dim3((unsigned)groups), dim3(NT), 0, s, a);
+    out(std::integral_constant<int, kScanFull>{}, (unsigned)groups);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(selective_scan_state, dim3((unsigned)(groups * (a.nch - 1))), dim3(NT), 0,
@@ -480,8 +574,7 @@ hipError_t launch_selective_scan(const ScanLaunch &L, hipStream_t s) {
   const int64_t lanes = L.batch * L.dim * ST;
   hipLaunchKernelGGL(selective_scan_carry, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0,
                      s, a, (int32_t)lanes);
-  hipLaunchKernelGGL(selective_scan_out<kScanOutput>, dim3((unsigned)(groups * a.nch)), dim3(NT),
-                     0, s, a);
+  out(std::integral_constant<int, kScanOutput>{}, (unsigned)(groups * a.nch));
   return hipGetLastError();
 }
 
