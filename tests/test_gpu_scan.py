@@ -5,11 +5,13 @@ alone exceeds 2e-2, so the criterion is |a - b| <= 2e-2 * max(1, |ref|)
 against the oracle's fp64 result rounded to bf16 (both sides are bf16).
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
 
-from helpers import bits, randn, to_f32
+from helpers import bits, randn, steady_scan_table, to_f32
 import oracle
 
 pytestmark = pytest.mark.gpu
@@ -174,3 +176,50 @@ def test_scan_softplus_branches(ops, b, d, L, softplus):
     assert np.isfinite(got).all()
     bad = np.abs(got - ref) > 2e-2 * np.maximum(1.0, np.abs(ref))
     assert not bad.any(), (np.argwhere(bad)[:5], np.abs(got - ref).max())
+
+
+@pytest.mark.parametrize("L", [(1 << 26) - 2, (1 << 26) - 1])
+def test_scan_longest_sequence_closed_form(L):
+    """seq_len just below the 2^26 limit, where a 16-channel block spans
+    nearly 2^31 bytes of the kernels' 32-bit offsets: the even length takes
+    the chunked path (about 1280 chunks), the odd one the single pass (one
+    work-group walking the whole sequence). The inputs have a closed form:
+    delta = 0.5 (softplus off), A = -1, B = C = 1, no D, no gate, and
+    u[c, t] = ((5 t + c) mod 9) - 4, so y[c, t] = 16 x_t of the recurrence in
+    helpers.steady_scan_table, which after 200 steps (e^-100 of the start left) is
+    periodic in t with a phase set by the channel. y starts as NaN, so an
+    output stored in the wrong place, or not stored, fails. The oracle is not
+    run: 2^26 steps of 256 recurrences is too long for it."""
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    from neptune_hip import _abi
+    d, n, warm = 16, 16, 200
+    _log(f"case: scan closed form d={d} L={L} ({'chunked' if _chunked(1, d, L) else 'single pass'})")
+    dev = "cuda"
+    t = torch.arange(L, device=dev, dtype=torch.int32)
+    u = torch.empty((1, d, L), dtype=torch.bfloat16, device=dev)
+    for c in range(d):
+        u[0, c] = ((5 * t + c) % 9 - 4).to(torch.bfloat16)
+    dr = torch.full((1, d, L), 0.5, dtype=torch.bfloat16, device=dev)
+    Bm = torch.ones((1, n, L), dtype=torch.bfloat16, device=dev)
+    Cm = torch.ones((1, n, L), dtype=torch.bfloat16, device=dev)
+    A = torch.full((d, n), -1.0, dtype=torch.float32, device=dev)
+    y = torch.full((1, d, L), float("nan"), dtype=torch.bfloat16, device=dev)
+    lib = _abi.load_library()
+    desc = _abi.ScanDesc(1, d, L, n, _abi.DTYPE_BF16, 0)
+    _abi.check(lib.neptune_selective_scan_fwd(
+        ctypes.byref(desc), u.data_ptr(), dr.data_ptr(), A.data_ptr(), Bm.data_ptr(), Cm.data_ptr(), None, None,
+        None, y.data_ptr(), torch.cuda.current_stream().cuda_stream), lib)
+    torch.cuda.synchronize()
+    del u, dr, Bm, Cm
+    head, period = steady_scan_table(d, warm)
+    phase = (t[warm:] - warm) % 9
+    for c in range(d):
+        got = y[0, c].float()
+        want = torch.empty(L, dtype=torch.float32, device=dev)
+        want[:warm] = torch.from_numpy(head[c]).float().to(dev)
+        want[warm:] = torch.from_numpy(period[c]).float().to(dev)[phase.long()]
+        assert bool(torch.isfinite(got).all()), f"channel {c}: an output was not stored"
+        err = (got - want).abs()
+        bad = err > 2e-2 * want.abs().clamp(min=1.0)
+        assert not bool(bad.any()), (c, int(bad.nonzero()[0]), float(err.max()))

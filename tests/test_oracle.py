@@ -17,7 +17,7 @@ import pytest
 import torch
 
 import oracle
-from helpers import bits, randn
+from helpers import bits, randn, steady_scan_table
 
 LN2 = math.log(2.0)
 LOG2E = 1.0 / LN2
@@ -533,6 +533,24 @@ def test_scan_closed_forms():
     bc = float(_f64(Bm)[0, :, 0] @ _f64(Cm)[0, :, 0])
     want = (bc * dl * uf[0, :, 0] + Df * uf[0, :, 0]) * gate[0, :, 0]
     assert np.abs(y1[0, :, 0] - want).max() < 1e-12
+
+
+def test_scan_closed_form_table_matches_oracle():
+    """The expected outputs of the longest-sequence GPU test come from
+    helpers.steady_scan_table; here they are held to the oracle on the same
+    inputs over 300 steps, past the 200 after which the test uses the
+    period."""
+    d, L, n, warm = 3, 300, 16, 200
+    t = np.arange(L)
+    u = torch.tensor(np.stack([((5 * t + c) % 9) - 4 for c in range(d)])[None],
+                     dtype=torch.bfloat16)
+    dr = torch.full((1, d, L), 0.5, dtype=torch.bfloat16)
+    ones = torch.ones((1, n, L), dtype=torch.bfloat16)
+    A = np.full((d, n), -1.0, dtype=np.float32)
+    _, y = oracle.selective_scan(bits(u), bits(dr), A, bits(ones), bits(ones), softplus=False)
+    head, period = steady_scan_table(d, warm)
+    want = np.concatenate([head, period[:, (t[warm:] - warm) % 9]], axis=1)
+    assert np.abs(y[0] - want).max() < 1e-9 * np.abs(want).max()
 
 
 def test_scan_linear_in_u():
