@@ -71,3 +71,40 @@ def steady_scan_table(d, warm):
                 period[c, t - warm] = 16.0 * x
     return head, period
 
+
+
+# Closed-form prefill inputs (test_gpu_edges' longest K^T sequence): K's
+# head_dim rows 0 and 127 and V, as functions of c = key index mod 35.
+def periodic_k0(c):
+    return (c % 5) - 2
+
+
+def periodic_k127(c):
+    return ((3 * (c % 7)) % 7) - 3
+
+
+def periodic_vper(c, d):
+    return ((c * (d + 1) + 1) % 13) - 6
+
+
+def periodic_attention(q0, S, scale):
+    """Exact O [rows, 128] and LSE [rows] of attention over S keys for query
+    rows q = q0[r] (e_0 + e_127), K[j, 0] = periodic_k0(j mod 35), K[j, 127] =
+    periodic_k127(j mod 35) and V[j, d] = periodic_vper(j mod 35, d), under
+    the HTile policy: P rounded to bf16 before P.V, the row sum over the
+    unrounded p, the running max fixed by the first key block (which holds
+    every residue). The sums take one term per residue mod 35 (float64)."""
+    c = np.arange(35)
+    count = S // 35 + (c < S % 35)
+    V = periodic_vper(c[:, None], np.arange(128)[None, :])
+    sc = np.float32(scale * 1.4426950408889634)
+    O, lse = [], []
+    for qr in q0:
+        s = (np.float32(qr) * (periodic_k0(c) + periodic_k127(c))).astype(np.float32)
+        m = np.float32(s.max() * sc)
+        p = np.exp2((s * sc - m).astype(np.float32).astype(np.float64))
+        p16 = torch.tensor(p, dtype=torch.float32).to(torch.bfloat16).double().numpy()
+        l = float((count * p).sum())
+        O.append((count * p16) @ V / l)
+        lse.append((float(m) + np.log2(l)) * np.log(2.0))
+    return np.array(O), np.array(lse)

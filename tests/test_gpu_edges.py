@@ -17,7 +17,8 @@ import torch
 
 import oracle
 from helpers import (TOL_BF16_ABS, TOL_FP8_ABS, TOL_LSE_ABS, bits, max_abs, oracle_dtype,
-                     randn, to_f32)
+                     periodic_attention, periodic_k0, periodic_k127, periodic_vper, randn,
+                     to_f32)
 
 pytestmark = pytest.mark.gpu
 
@@ -129,3 +130,48 @@ def test_scan_short_sequences(ops, L):
     got = to_f32(y).astype(np.float64)
     assert np.isfinite(got).all()
     assert (np.abs(got - ref) <= 2e-2 * np.maximum(1.0, np.abs(ref))).all()
+
+
+def test_prefill_longest_kt_keys_closed_form(ops):
+    """K stored [B, H, D, S] (k_dim_order = 1) at the longest seq_kv the
+    head_dim-128 kernel accepts there: 127 S 2 + 256 < 2^32 bytes of per-lane
+    offset, S = 16,909,312 (a multiple of 8). The last head_dim row of a K^T
+    tile then sits nearly 4 GiB past the tile's base. Four query rows
+    q = 2 (r + 1) (e_0 + e_127) score key j by K's rows 0 and 127 (periods 5
+    and 7 in j; the other rows carry other patterns that q does not see), and
+    V is periodic in j with period 35, so O and the LSE have the closed form
+    of helpers.periodic_attention. A K row or key read from the wrong place
+    changes the pairing of scores and values and fails; the oracle is not run
+    over 16.9M keys."""
+    S, D, rows = 16_909_312, 128, 4
+    assert 127 * S * 2 + 256 < 1 << 32 <= 127 * (S + 8) * 2 + 256
+    _log(f"case: prefill d128 k_dim_order=1 closed form Sk={S}")
+    dev = "cuda"
+    jm = torch.arange(S, device=dev, dtype=torch.int32) % 35
+    kt = torch.empty((1, 1, D, S), dtype=torch.bfloat16, device=dev)
+    kt[0, 0, 0] = periodic_k0(jm).to(torch.bfloat16)
+    kt[0, 0, D - 1] = periodic_k127(jm).to(torch.bfloat16)
+    for d in range(1, D - 1):
+        kt[0, 0, d] = ((jm + d) % 11 - 5).to(torch.bfloat16)
+    v = torch.empty((1, 1, S, D), dtype=torch.bfloat16, device=dev)
+    dcol = torch.arange(D, device=dev, dtype=torch.int32)
+    step = 1 << 21
+    for s0 in range(0, S, step):
+        v[0, 0, s0:s0 + step] = periodic_vper(jm[s0:s0 + step, None], dcol[None, :]).to(
+            torch.bfloat16)
+    del jm
+    q0 = [2.0 * (r + 1) for r in range(rows)]
+    q = torch.zeros((1, 1, rows, D), dtype=torch.bfloat16, device=dev)
+    q[0, 0, :, 0] = torch.tensor(q0, dtype=torch.bfloat16)
+    q[0, 0, :, D - 1] = torch.tensor(q0, dtype=torch.bfloat16)
+    out, lse = ops.attention(q, kt, v, return_lse=True, k_dim_order=1)
+    torch.cuda.synchronize()
+    want_o, want_lse = periodic_attention(q0, S, 1.0 / np.sqrt(D))
+    got_o, got_lse = to_f32(out)[0, 0], to_f32(lse)[0, 0]
+    assert np.isfinite(got_o).all()
+    # |O| reaches 5 here, and both the bf16 rounding of P (where v_exp_f32's
+    # last bit can flip it) and that of O are relative: 2e-2 of max(1, |O|),
+    # against changes of order 1 from a misplaced row or key
+    err = np.abs(got_o - want_o)
+    assert (err <= TOL_BF16_ABS * np.maximum(1.0, np.abs(want_o))).all(), err.max()
+    assert max_abs(got_lse, want_lse) <= TOL_LSE_ABS, (got_lse, want_lse)

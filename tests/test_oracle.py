@@ -17,7 +17,8 @@ import pytest
 import torch
 
 import oracle
-from helpers import bits, randn, steady_scan_table
+from helpers import (bits, periodic_attention, periodic_k0, periodic_k127, periodic_vper, randn,
+                     steady_scan_table)
 
 LN2 = math.log(2.0)
 LOG2E = 1.0 / LN2
@@ -551,6 +552,33 @@ def test_scan_closed_form_table_matches_oracle():
     head, period = steady_scan_table(d, warm)
     want = np.concatenate([head, period[:, (t[warm:] - warm) % 9]], axis=1)
     assert np.abs(y[0] - want).max() < 1e-9 * np.abs(want).max()
+
+
+def test_periodic_attention_closed_form_matches_oracle():
+    """The expected outputs of the longest-K^T prefill GPU test come from
+    helpers.periodic_attention; here they are held to the oracle's HTile
+    attention on the same construction over 1000 keys (28 full periods and a
+    partial one), and its residue counting to a direct sum over the keys."""
+    S, D, q0 = 1000, 128, [2.0, 8.0]
+    c = np.arange(S) % 35
+    K = np.zeros((S, D))
+    K[:, 0], K[:, D - 1] = periodic_k0(c), periodic_k127(c)
+    K[:, 1:D - 1] = (c[:, None] + np.arange(1, D - 1)[None, :]) % 11 - 5
+    V = periodic_vper(c[:, None], np.arange(D)[None, :])
+    Q = np.zeros((len(q0), D))
+    Q[:, 0] = Q[:, D - 1] = q0
+    q, k, v = (torch.tensor(a[None, None], dtype=torch.bfloat16) for a in (Q, K, V))
+    o, lse = oracle.attn_fwd(bits(q), bits(k), bits(v), oracle.BF16, False, 0.0)
+    want_o, want_lse = periodic_attention(q0, S, 1.0 / math.sqrt(D))
+    got = oracle.decode(o, oracle.BF16)[0, 0]
+    assert np.abs(got - want_o).max() <= 2.0 ** -8 * np.abs(want_o).max()
+    assert np.abs(lse[0, 0] - want_lse).max() < 1e-5
+    # the residue sums against the sums over every key
+    sc = np.float32(1.0 / math.sqrt(D) * 1.4426950408889634)
+    s = (np.float32(q0[1]) * (periodic_k0(c) + periodic_k127(c))).astype(np.float32)
+    p = np.exp2((s * sc - np.float32(s.max() * sc)).astype(np.float32).astype(np.float64))
+    p16 = torch.tensor(p, dtype=torch.float32).to(torch.bfloat16).double().numpy()
+    assert np.abs(p16 @ V / p.sum() - want_o[1]).max() < 1e-12
 
 
 def test_scan_linear_in_u():
