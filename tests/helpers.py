@@ -73,8 +73,9 @@ def steady_scan_table(d, warm):
 
 
 
-# Closed-form prefill inputs (test_gpu_edges' longest K^T sequence): K's
-# head_dim rows 0 and 127 and V, as functions of c = key index mod 35.
+# Closed-form attention inputs (the longest-sequence prefill and decode
+# tests): K's head_dim rows 0 and 127 and V as functions of c = key index
+# mod 35, plus a step in V per 2^seg_bits keys.
 def periodic_k0(c):
     return (c % 5) - 2
 
@@ -87,15 +88,25 @@ def periodic_vper(c, d):
     return ((c * (d + 1) + 1) % 13) - 6
 
 
-def periodic_attention(q0, S, scale):
+def residue_counts(a, b, m=35):
+    """How many j in [a, b) have j mod m = c, for c = 0 .. m - 1."""
+    c = np.arange(m)
+    return (b - 1 - c) // m - (a - 1 - c) // m
+
+
+def periodic_attention(q0, S, scale, seg_shift=0, seg_bits=24):
     """Exact O [rows, 128] and LSE [rows] of attention over S keys for query
-    rows q = q0[r] (e_0 + e_127), K[j, 0] = periodic_k0(j mod 35), K[j, 127] =
-    periodic_k127(j mod 35) and V[j, d] = periodic_vper(j mod 35, d), under
-    the HTile policy: P rounded to bf16 before P.V, the row sum over the
-    unrounded p, the running max fixed by the first key block (which holds
-    every residue). The sums take one term per residue mod 35 (float64)."""
+    rows q = q0[r] (e_0 + e_127), K[j, 0] = periodic_k0(j mod 35),
+    K[j, 127] = periodic_k127(j mod 35) and V[j, d] = periodic_vper(j mod 35,
+    d) + seg_shift (j >> seg_bits), under the HTile policy: P rounded to bf16
+    before P.V, the row sum over the unrounded p, the running max fixed by
+    the first key block (which holds every residue). The sums take one term
+    per residue mod 35 and segment (float64)."""
     c = np.arange(35)
-    count = S // 35 + (c < S % 35)
+    count = residue_counts(0, S)
+    segsum = np.zeros(35)  # per residue: the segment indices of its keys, summed
+    for s in range(1, -(-S >> seg_bits)):
+        segsum += s * residue_counts(s << seg_bits, min((s + 1) << seg_bits, S))
     V = periodic_vper(c[:, None], np.arange(128)[None, :])
     sc = np.float32(scale * 1.4426950408889634)
     O, lse = [], []
@@ -105,6 +116,6 @@ def periodic_attention(q0, S, scale):
         p = np.exp2((s * sc - m).astype(np.float32).astype(np.float64))
         p16 = torch.tensor(p, dtype=torch.float32).to(torch.bfloat16).double().numpy()
         l = float((count * p).sum())
-        O.append((count * p16) @ V / l)
+        O.append(((count * p16) @ V + seg_shift * float(segsum @ p16)) / l)
         lse.append((float(m) + np.log2(l)) * np.log(2.0))
     return np.array(O), np.array(lse)

@@ -13,7 +13,8 @@ import torch
 
 import oracle
 from helpers import (TOL_BF16_ABS, TOL_FP8_ABS, TOL_LSE_ABS, bits, from_bf16_bits, max_abs,
-                     randn, to_f32)
+                     periodic_attention, periodic_k0, periodic_k127, periodic_vper, randn,
+                     to_f32)
 
 pytestmark = pytest.mark.gpu
 
@@ -206,3 +207,97 @@ def test_workspace_too_small(ops):
     ws = torch.empty(16, dtype=torch.uint8, device="cuda")
     with pytest.raises(NeptuneWorkspaceTooSmall):
         ops.decode_splitk(q, k, k, workspace=ws)
+
+
+
+SEG_STEP = 4.0  # V's step per 2^24 tokens (4 GiB of 256-byte rows)
+
+
+def _periodic_kv_rows(t0, t1, dev):
+    """K and V rows [t1 - t0, 128] bf16 of tokens t0 .. t1 - 1 for the
+    closed-form decode tests: K's head_dim rows 0 and 127 and V periodic in
+    the token index (helpers.periodic_*), V stepped by SEG_STEP every 2^24
+    tokens, K's other rows a period-11 pattern the queries do not see."""
+    D = 128
+    dcol = torch.arange(D, device=dev, dtype=torch.int32)
+    j = torch.arange(t0, t1, device=dev, dtype=torch.int32)
+    jm = j % 35
+    krows = (jm[:, None] + dcol[None, :]) % 11 - 5
+    krows[:, 0] = periodic_k0(jm)
+    krows[:, D - 1] = periodic_k127(jm)
+    vrows = periodic_vper(jm[:, None], dcol[None, :]) + int(SEG_STEP) * (j >> 24)[:, None]
+    return krows.to(torch.bfloat16), vrows.to(torch.bfloat16)
+
+
+def _periodic_queries(q0, dev):
+    q = torch.zeros((1, len(q0), 128), dtype=torch.bfloat16, device=dev)
+    q[0, :, 0] = torch.tensor(q0, dtype=torch.bfloat16)
+    q[0, :, 127] = torch.tensor(q0, dtype=torch.bfloat16)
+    return q
+
+
+def _check_periodic(o, lse, q0, L):
+    want_o, want_lse = periodic_attention(q0, L, 1.0 / np.sqrt(128), seg_shift=SEG_STEP)
+    got_o, got_lse = to_f32(o)[0], to_f32(lse)[0]
+    assert np.isfinite(got_o).all()
+    err = np.abs(got_o - want_o)
+    assert (err <= TOL_BF16_ABS * np.maximum(1.0, np.abs(want_o))).all(), err.max()
+    assert max_abs(got_lse, want_lse) <= TOL_LSE_ABS, (got_lse, want_lse)
+
+
+def test_decode_16gib_head_closed_form(ops):
+    """One KV head of 2^26 + 37 tokens (16 GiB each for K and V, past every
+    32-bit byte offset) read by a GQA group of four query heads over 1024
+    splits. Query head h is q0[h] (e_0 + e_127); K's head_dim rows 0 and 127
+    and V are periodic in the token index with period 35 (coprime to the
+    32-token step), V steps up every 2^24 tokens (every 4 GiB), K's other
+    rows carry a pattern q does not see, so O and the LSE have the closed
+    form of helpers.periodic_attention (P's bf16 rounding included; each
+    split's own running max changes that rounding by a relative 2^-8 at
+    most). A token read from the wrong place changes the pairing of scores
+    and values, and one read 4 GiB low loses a step; either fails. The
+    oracle is not run over 67M tokens."""
+    L, D, q0 = (1 << 26) + 37, 128, [2.0, 4.0, 6.0, 8.0]
+    _log(f"case: decode bf16 closed form L={L} Hq=4 Hkv=1 splits=1024")
+    dev = "cuda"
+    k = torch.empty((1, 1, L, D), dtype=torch.bfloat16, device=dev)
+    v = torch.empty((1, 1, L, D), dtype=torch.bfloat16, device=dev)
+    step = 1 << 21
+    for t0 in range(0, L, step):
+        t1 = min(t0 + step, L)
+        k[0, 0, t0:t1], v[0, 0, t0:t1] = _periodic_kv_rows(t0, t1, dev)
+    o, lse = ops.decode_splitk(_periodic_queries(q0, dev), k, v, num_splits=1024, return_lse=True)
+    torch.cuda.synchronize()
+    _check_periodic(o, lse, q0, L)
+
+
+def test_decode_paged_16gib_pool_closed_form(ops):
+    """The same 2^26 + 37 tokens in a pool of 64-token pages (16 GiB for K,
+    16 for V), logical page i stored at page (i + 12345) mod pages: page
+    bases lie past every 32-bit byte offset, the block table is not the
+    identity, and the last page is partly filled. A page base that wrapped at
+    4 GiB would read the pages 2^24 tokens earlier, a step lower in V."""
+    L, D, q0, P = (1 << 26) + 37, 128, [2.0, 4.0, 6.0, 8.0], 64
+    npages = -(-L // P)
+    _log(f"case: decode paged bf16 closed form L={L} pages={npages} rotated")
+    dev = "cuda"
+    perm = (torch.arange(npages, device=dev) + 12345) % npages
+    kp = torch.zeros((npages, 1, P, D), dtype=torch.bfloat16, device=dev)
+    vp = torch.zeros((npages, 1, P, D), dtype=torch.bfloat16, device=dev)
+    step = 1 << 15  # pages per fill
+    for p0 in range(0, npages, step):
+        p1 = min(p0 + step, npages)
+        t1 = min(p1 * P, L)
+        kr, vr = _periodic_kv_rows(p0 * P, t1, dev)
+        pad = p1 * P - t1
+        if pad:
+            kr = torch.cat([kr, torch.zeros((pad, D), dtype=kr.dtype, device=dev)])
+            vr = torch.cat([vr, torch.zeros((pad, D), dtype=vr.dtype, device=dev)])
+        kp[perm[p0:p1]] = kr.view(p1 - p0, 1, P, D)
+        vp[perm[p0:p1]] = vr.view(p1 - p0, 1, P, D)
+    table = perm.to(torch.int32)[None]
+    lens = torch.tensor([L], dtype=torch.int32, device=dev)
+    o, lse = ops.decode_paged(_periodic_queries(q0, dev), kp, vp, table, lens, num_splits=1024,
+                              return_lse=True)
+    torch.cuda.synchronize()
+    _check_periodic(o, lse, q0, L)

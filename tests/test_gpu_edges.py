@@ -139,10 +139,11 @@ def test_prefill_longest_kt_keys_closed_form(ops):
     tile then sits nearly 4 GiB past the tile's base. Four query rows
     q = 2 (r + 1) (e_0 + e_127) score key j by K's rows 0 and 127 (periods 5
     and 7 in j; the other rows carry other patterns that q does not see), and
-    V is periodic in j with period 35, so O and the LSE have the closed form
-    of helpers.periodic_attention. A K row or key read from the wrong place
-    changes the pairing of scores and values and fails; the oracle is not run
-    over 16.9M keys."""
+    V is periodic in j with period 35 plus a step of 32 at key 2^24 (V's
+    first 4 GiB end there), so O and the LSE have the closed form of
+    helpers.periodic_attention. A K row or key read from the wrong place
+    changes the pairing of scores and values, and a V row read 4 GiB low
+    loses the step; either fails. The oracle is not run over 16.9M keys."""
     S, D, rows = 16_909_312, 128, 4
     assert 127 * S * 2 + 256 < 1 << 32 <= 127 * (S + 8) * 2 + 256
     _log(f"case: prefill d128 k_dim_order=1 closed form Sk={S}")
@@ -157,8 +158,9 @@ def test_prefill_longest_kt_keys_closed_form(ops):
     dcol = torch.arange(D, device=dev, dtype=torch.int32)
     step = 1 << 21
     for s0 in range(0, S, step):
-        v[0, 0, s0:s0 + step] = periodic_vper(jm[s0:s0 + step, None], dcol[None, :]).to(
-            torch.bfloat16)
+        seg = 32 * (torch.arange(s0, min(s0 + step, S), device=dev, dtype=torch.int32) >> 24)
+        v[0, 0, s0:s0 + step] = (periodic_vper(jm[s0:s0 + step, None], dcol[None, :]) +
+                                 seg[:, None]).to(torch.bfloat16)
     del jm
     q0 = [2.0 * (r + 1) for r in range(rows)]
     q = torch.zeros((1, 1, rows, D), dtype=torch.bfloat16, device=dev)
@@ -166,7 +168,7 @@ def test_prefill_longest_kt_keys_closed_form(ops):
     q[0, 0, :, D - 1] = torch.tensor(q0, dtype=torch.bfloat16)
     out, lse = ops.attention(q, kt, v, return_lse=True, k_dim_order=1)
     torch.cuda.synchronize()
-    want_o, want_lse = periodic_attention(q0, S, 1.0 / np.sqrt(D))
+    want_o, want_lse = periodic_attention(q0, S, 1.0 / np.sqrt(D), seg_shift=32.0)
     got_o, got_lse = to_f32(out)[0, 0], to_f32(lse)[0, 0]
     assert np.isfinite(got_o).all()
     # |O| reaches 5 here, and both the bf16 rounding of P (where v_exp_f32's

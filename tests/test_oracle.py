@@ -555,10 +555,11 @@ def test_scan_closed_form_table_matches_oracle():
 
 
 def test_periodic_attention_closed_form_matches_oracle():
-    """The expected outputs of the longest-K^T prefill GPU test come from
-    helpers.periodic_attention; here they are held to the oracle's HTile
-    attention on the same construction over 1000 keys (28 full periods and a
-    partial one), and its residue counting to a direct sum over the keys."""
+    """The expected outputs of the longest-sequence prefill and decode GPU
+    tests come from helpers.periodic_attention; here they are held to the
+    oracle's HTile attention on the same construction over 1000 keys (28
+    full periods and a partial one), and its residue and segment counting to
+    a direct sum over the keys."""
     S, D, q0 = 1000, 128, [2.0, 8.0]
     c = np.arange(S) % 35
     K = np.zeros((S, D))
@@ -573,12 +574,15 @@ def test_periodic_attention_closed_form_matches_oracle():
     got = oracle.decode(o, oracle.BF16)[0, 0]
     assert np.abs(got - want_o).max() <= 2.0 ** -8 * np.abs(want_o).max()
     assert np.abs(lse[0, 0] - want_lse).max() < 1e-5
-    # the residue sums against the sums over every key
+    # the residue and segment sums against the sums over every key, with a
+    # step of 4 in V every 64 keys standing in for every 2^24
     sc = np.float32(1.0 / math.sqrt(D) * 1.4426950408889634)
     s = (np.float32(q0[1]) * (periodic_k0(c) + periodic_k127(c))).astype(np.float32)
     p = np.exp2((s * sc - np.float32(s.max() * sc)).astype(np.float32).astype(np.float64))
     p16 = torch.tensor(p, dtype=torch.float32).to(torch.bfloat16).double().numpy()
-    assert np.abs(p16 @ V / p.sum() - want_o[1]).max() < 1e-12
+    Vseg = V + 4.0 * (np.arange(S) >> 6)[:, None]
+    seg_o, _ = periodic_attention(q0[1:], S, 1.0 / math.sqrt(D), seg_shift=4.0, seg_bits=6)
+    assert np.abs(p16 @ Vseg / p.sum() - seg_o[0]).max() < 1e-12
 
 
 def test_scan_linear_in_u():
