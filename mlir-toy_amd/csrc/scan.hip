@@ -69,11 +69,11 @@
 //
 // Sequence-parallel path. When batch * dim / 16 work-groups cannot fill the
 // GPU (few channels, long sequences), the sequence is cut into nch chunks of
-// T steps (the last one takes the remainder, T .. 2T - 1 steps) and the
+// nearly equal length (whole 32-step units, at least two per chunk) and the
 // scan runs in three launches, using y itself as scratch (no workspace):
 //   state   every chunk but the last scans from x = 0 without outputs and
 //           leaves its end state x_end[16] and its delta sum S (fp32) at the
-//           start of its own y segment (T >= 64 steps: 128 bytes >= 68);
+//           start of its own y segment (64 steps or more: 128 bytes >= 68);
 //   carry   one lane per (batch, channel, state) walks the chunks in order,
 //           x_start[k + 1] = 2^(A S[k] log2 e) x_start[k] + x_end[k] (the
 //           decay over a chunk is the product of its steps' decays), and
@@ -104,7 +104,10 @@ struct ScanArgs {
   uint16_t *y;
   int32_t Dm, L, softplus;
   int32_t vec;  // 4-byte pair access: L even and every base 4-byte aligned
-  int32_t T, nch;  // chunk length and count (1 chunk of L: the single pass)
+  // chunks of the sequence (1: the single pass): chunk k starts at step
+  // chunk_start(k); the first rem hold Tu + 1 units of 32 steps, the others Tu
+  // (the last also the partial unit at the end)
+  int32_t Tu, rem, nch;
 };
 
 // the output kernel as the single pass, and as the chunked path's output pass
@@ -112,8 +115,11 @@ enum ScanMode { kScanFull = 0, kScanOutput = 1 };
 
 // chunk k of channel d of batch row b: its y segment as fp32 scratch
 // (x[16], then S)
+__device__ inline int chunk_start(const ScanArgs &a, int k) {
+  return TT * (k * a.Tu + min(k, a.rem));
+}
 __device__ inline float *chunk_scratch(const ScanArgs &a, int b, int d, int k) {
-  return reinterpret_cast<float *>(a.y + ((int64_t)b * a.Dm + d) * a.L + (int64_t)k * a.T);
+  return reinterpret_cast<float *>(a.y + ((int64_t)b * a.Dm + d) * a.L + chunk_start(a, k));
 }
 
 __device__ inline float lo_bf16(uint32_t p) { return __uint_as_float(p << 16); }
@@ -148,8 +154,8 @@ __global__ __launch_bounds__(NT) void selective_scan_state(ScanArgs a) {
   const int grp = (int)(blockIdx.x / (unsigned)nwch);
   const int b = grp / nblk;
   const int d0 = (grp % nblk) * SCH;
-  const int tb = kc * a.T;
-  const int te = tb + a.T;
+  const int tb = chunk_start(a, kc);
+  const int te = chunk_start(a, kc + 1);
 
   // scan identity: channel c, state n
   const int c = lane & 15, r = lane >> 4;
@@ -297,8 +303,8 @@ __global__ __launch_bounds__(NT, 5) void selective_scan_out(ScanArgs a) {
   const int grp = (int)(blockIdx.x / (unsigned)a.nch);
   const int b = __builtin_amdgcn_readfirstlane(grp / nblk);
   const int d0 = __builtin_amdgcn_readfirstlane((grp % nblk) * SCH);
-  const int tb = kc * a.T;
-  const int te = kc == a.nch - 1 ? a.L : tb + a.T;
+  const int tb = chunk_start(a, kc);
+  const int te = kc == a.nch - 1 ? a.L : chunk_start(a, kc + 1);
 
   const int q = lane >> 4, n = lane & 15;
   const int ch = d0 + 4 * w + q;  // this lane's channel
@@ -465,30 +471,51 @@ __global__ __launch_bounds__(NT, 5) void selective_scan_out(ScanArgs a) {
 
 // The carry pass: one lane per (batch row, channel, state) walks the chunks
 // in order and leaves each chunk's starting state where its end state was.
+// The walk depends on memory only through the chunk summaries, which do not
+// depend on it: they are read KB chunks at a time, one batch ahead of the
+// walk, in two register sets, so a sequence cut into hundreds of chunks
+// waits on memory about once rather than once per chunk. A batch is read
+// before any of its chunks is written (the summary a lane reads and the
+// starting state it writes share the chunk's slot n).
+constexpr int KB = 16;
 __global__ __launch_bounds__(256) void selective_scan_carry(ScanArgs a, int32_t lanes) {
   const int gid = blockIdx.x * 256 + threadIdx.x;
   if (gid >= lanes) return;
   const int n = gid & (ST - 1), bd = gid / ST;
   const int b = bd / a.Dm, d = bd - b * a.Dm;
   const float A2 = a.A[(int64_t)d * ST + n] * kLog2e;
-  float carry = 0.0f;
-  float *p = chunk_scratch(a, b, d, 0);
-  float xe = p[n], S = p[ST];
-  for (int k = 0; k + 1 < a.nch; ++k) {
-    // the next chunk's summary is read before this chunk's is overwritten
-    float *pn = chunk_scratch(a, b, d, k + 1);
-    float xe_n = 0.0f, S_n = 0.0f;
-    if (k + 2 < a.nch) {
-      xe_n = pn[n];
-      S_n = pn[ST];
+  const int nsum = a.nch - 1;  // chunks with a summary: all but the last
+  float xe[2][KB], S[2][KB];
+  auto load = [&](auto SET, int k0) {
+    constexpr int set = decltype(SET)::value;
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+      // past the last summary: re-read it (the value is not used)
+      const float *p = chunk_scratch(a, b, d, min(k0 + i, nsum - 1));
+      xe[set][i] = p[n];
+      S[set][i] = p[ST];
     }
-    p[n] = carry;
-    carry = fmaf(fast_exp2(A2 * S), carry, xe);
-    p = pn;
-    xe = xe_n;
-    S = S_n;
+  };
+  float carry = 0.0f;
+  auto walk = [&](auto SET, int k0) {
+    constexpr int set = decltype(SET)::value;
+#pragma unroll
+    for (int i = 0; i < KB; ++i)
+      if (k0 + i < nsum) {
+        chunk_scratch(a, b, d, k0 + i)[n] = carry;
+        carry = fmaf(fast_exp2(A2 * S[set][i]), carry, xe[set][i]);
+      }
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  load(S0{}, 0);
+  for (int k0 = 0; k0 < nsum; k0 += 2 * KB) {
+    load(S1{}, k0 + KB);
+    walk(S0{}, k0);
+    load(S0{}, k0 + 2 * KB);
+    walk(S1{}, k0 + KB);
   }
-  p[n] = carry;  // the last chunk's starting state
+  chunk_scratch(a, b, d, nsum)[n] = carry;  // the last chunk's starting state
 }
 
 }  // namespace
@@ -497,26 +524,28 @@ __global__ __launch_bounds__(256) void selective_scan_carry(ScanArgs a, int32_t 
 // launch fewer than kScanFillGroups work-groups (four per CU) and the
 // sequence holds at least two 64-step chunks; the chunk count brings the
 // launch to about kScanTargetGroups work-groups (five per CU, what the
-// single pass gets at config 4). T is a multiple of 32 steps and at least
-// 64; the last chunk takes the remainder (T .. 2T - 1 steps). nch = 1: the
-// single pass. The chunked path needs the 4-byte pair access (even L).
+// single pass gets at config 4). The whole 32-step units of the sequence
+// are dealt out evenly: every chunk holds Tu or Tu + 1 units (Tu >= 2), the
+// last one also the partial unit at the end, so no chunk holds up its
+// launch by more than 32 steps. nch = 1: the single pass. The chunked path
+// needs the 4-byte pair access (even L).
 constexpr int64_t kScanFillGroups = 1024, kScanTargetGroups = 1280, kScanMinChunk = 64;
 constexpr int64_t kScanMaxSeq = (int64_t)1 << 26;  // 16 rows x 2 bytes x 2^26 = 2^31
 
-void scan_chunking(int64_t batch, int64_t dim, int64_t L, bool vec, int32_t *T, int32_t *nch) {
+void scan_chunking(int64_t batch, int64_t dim, int64_t L, bool vec, int32_t *Tu, int32_t *rem,
+                   int32_t *nch) {
   const int64_t groups = (dim + SCH - 1) / SCH * batch;
-  *T = (int32_t)L;
+  *Tu = 0;
+  *rem = 0;
   *nch = 1;
   if (!vec || groups >= kScanFillGroups || L < 2 * kScanMinChunk) return;
+  const int64_t units = L / TT;
   int64_t want = (kScanTargetGroups + groups - 1) / groups;
-  want = std::min(want, L / kScanMinChunk);
+  want = std::min(want, units / (kScanMinChunk / TT));
   if (want < 2) return;
-  int64_t t = (L + want - 1) / want;
-  t = std::max<int64_t>((t + TT - 1) / TT * TT, kScanMinChunk);
-  const int64_t k = L / t;  // the last chunk absorbs the remainder
-  if (k < 2) return;
-  *T = (int32_t)t;
-  *nch = (int32_t)k;
+  *nch = (int32_t)want;
+  *Tu = (int32_t)(units / want);
+  *rem = (int32_t)(units % want);
 }
 
 bool scan_supported(const ScanLaunch &a, const char **why) {
@@ -556,7 +585,7 @@ hipError_t launch_selective_scan(const ScanLaunch &L, hipStream_t s) {
   a.vec = (L.seq_len % 2 == 0) && al4(L.u) && al4(L.delta_raw) && al4(L.B) && al4(L.C) &&
           al4(L.y) && (!L.z || al4(L.z));
   const int64_t groups = (L.dim + SCH - 1) / SCH * L.batch;
-  scan_chunking(L.batch, L.dim, L.seq_len, a.vec != 0, &a.T, &a.nch);
+  scan_chunking(L.batch, L.dim, L.seq_len, a.vec != 0, &a.Tu, &a.rem, &a.nch);
   const bool sp = L.delta_softplus != 0, gate = L.z != nullptr;
   // the output kernel for this mode and these options
   auto out = [&](auto mode, unsigned grid) {
