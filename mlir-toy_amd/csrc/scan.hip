@@ -518,6 +518,48 @@ __global__ __launch_bounds__(256) void selective_scan_carry(ScanArgs a, int32_t 
   chunk_scratch(a, b, d, nsum)[n] = carry;  // the last chunk's starting state
 }
 
+// The carry pass for long chains of chunks (more than 64 summaries): one
+// wave per (batch row, channel, state), 64 chunks per pass, one per lane.
+// Chunk k maps its starting state x to a_k x + b_k (a_k = 2^(A S_k log2 e),
+// b_k its end state from 0); an inclusive scan of these affine maps across
+// the lanes (Hillis-Steele, six shuffles) gives every lane the map from the
+// pass's starting state to the end of its chunk, so its chunk's starting
+// state is the previous lane's map applied to that state. The pass's loads
+// are independent, so a chain of hundreds of chunks waits on memory once
+// per 64 chunks. Lanes past the last summary carry the identity map.
+__global__ __launch_bounds__(256) void selective_scan_carry_wave(ScanArgs a, int32_t rows) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const int n = row & (ST - 1), bd = row / ST;
+  const int b = bd / a.Dm, d = bd - b * a.Dm;
+  const float A2 = a.A[(int64_t)d * ST + n] * kLog2e;
+  const int nsum = a.nch - 1;
+  float carry = 0.0f;  // the state at the start of the pass (the same in every lane)
+  for (int k0 = 0; k0 < nsum; k0 += 64) {
+    const int k = k0 + lane;
+    const bool live = k < nsum;
+    const float *p = chunk_scratch(a, b, d, live ? k : nsum - 1);
+    float m = live ? fast_exp2(A2 * p[ST]) : 1.0f;  // this lane's map: x -> m x + c
+    float c = live ? p[n] : 0.0f;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      // compose with the map of the lanes before: x -> m (m' x + c') + c
+      const float mp = __shfl_up(m, off, 64), cp = __shfl_up(c, off, 64);
+      if (lane >= off) {
+        c = fmaf(m, cp, c);
+        m *= mp;
+      }
+    }
+    // this chunk starts where the lanes before it end
+    const float mp = __shfl_up(m, 1, 64), cp = __shfl_up(c, 1, 64);
+    const float start = lane == 0 ? carry : fmaf(mp, carry, cp);
+    if (live) chunk_scratch(a, b, d, k)[n] = start;
+    carry = fmaf(__shfl(m, 63, 64), carry, __shfl(c, 63, 64));
+  }
+  if (lane == 0) chunk_scratch(a, b, d, nsum)[n] = carry;  // the last chunk's starting state
+}
+
 }  // namespace
 
 // Chunking of the sequence-parallel path: used when the single pass would
@@ -601,8 +643,14 @@ hipError_t launch_selective_scan(const ScanLaunch &L, hipStream_t s) {
   hipLaunchKernelGGL(selective_scan_state, dim3((unsigned)(groups * (a.nch - 1))), dim3(NT), 0,
                      s, a);
   const int64_t lanes = L.batch * L.dim * ST;
-  hipLaunchKernelGGL(selective_scan_carry, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0,
-                     s, a, (int32_t)lanes);
+  // a long chain of chunks: one wave per (batch, channel, state); up to 64
+  // summaries the per-lane walk measured as fast or faster
+  if (a.nch - 1 > 4 * KB)
+    hipLaunchKernelGGL(selective_scan_carry_wave, dim3((unsigned)((lanes + 3) / 4)), dim3(256), 0,
+                       s, a, (int32_t)lanes);
+  else
+    hipLaunchKernelGGL(selective_scan_carry, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0,
+                       s, a, (int32_t)lanes);
   out(std::integral_constant<int, kScanOutput>{}, (unsigned)(groups * a.nch));
   return hipGetLastError();
 }
