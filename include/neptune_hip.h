@@ -139,9 +139,13 @@ typedef struct neptune_paged_kv_desc {
  *   x_n  <- exp(delta * A[d,n]) x_n + delta * B[b,n,l] * u[b,d,l]
  *   y     = (sum_n C[b,n,l] x_n + D[d] u) * silu(z)      (z nullable)
  * u, delta_raw, z, y [batch, dim, seq_len]; B, C [batch, d_state, seq_len]
- * in io_dtype (BF16); A [dim, d_state], D and delta_bias [dim] fp32. The
- * state is carried in fp32 from x = 0. Supported: d_state 16 and seq_len
- * below 2^26 (NEPTUNE_ERR_UNSUPPORTED otherwise). */
+ * in io_dtype (BF16); A [dim, d_state], D and delta_bias [dim] fp32 (D,
+ * z and delta_bias may be NULL: no skip term, no gate, no bias). The state
+ * is carried in fp32 from x = 0. y must not overlap any input: the call
+ * writes y while it still reads later steps, and for few channels over a
+ * long sequence it keeps per-chunk state in y before the outputs overwrite
+ * it (no workspace). Supported: d_state 16 and seq_len below 2^26
+ * (NEPTUNE_ERR_UNSUPPORTED otherwise). */
 typedef struct neptune_scan_desc {
   int64_t batch, dim, seq_len, d_state;
   int32_t io_dtype;        /* BF16 */
