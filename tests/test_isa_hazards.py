@@ -15,6 +15,11 @@ it in program order. It pins a paged-decode bug in which a base looked up
 in the block table was written by ``v_readfirstlane`` two instructions
 before the copy that read it. The copy saw the previous base and loaded
 another step's tokens, with no fault.
+
+The same compiled code also holds the kernels to the register budgets their
+speed depends on (test_kernel_register_budgets): the selective scan's
+output kernel within 96 VGPRs (five waves per SIMD), the production prefill
+within 256 (two per SIMD), and these and the decode kernels without scratch.
 """
 
 from __future__ import annotations
@@ -166,20 +171,31 @@ def test_checker_flags_a_stale_base():
     assert hazards("\ts_mov_b32 m0, s4\n\tglobal_load_dwordx4 v[4:7], v[2:3], off\n") == []
 
 
-@pytest.mark.skipif(not Path(HIPCC).exists(), reason="hipcc not available")
-def test_lds_dma_wait_states(tmp_path):
+@pytest.fixture(scope="module")
+def compiled(tmp_path_factory):
+    """Every kernel source compiled to gfx950 assembly with the build's flags
+    (file name -> assembly text)."""
+    if not Path(HIPCC).exists():
+        pytest.skip("hipcc not available")
+    tmp = tmp_path_factory.mktemp("isa")
     flags = _build_flags()
     procs = {}
     for src in SOURCES:
-        out = tmp_path / (src.stem + ".s")
+        out = tmp / (src.stem + ".s")
         procs[src.name] = (out, subprocess.Popen(
             [HIPCC, *flags, "--cuda-device-only", "-S", "-o", str(out), str(src)],
             stdout=subprocess.DEVNULL, stderr=subprocess.PIPE, text=True))
-    report, copies, kwaits = [], 0, 0
+    asm = {}
     for name, (out, p) in procs.items():
         _, err = p.communicate(timeout=600)
         assert p.returncode == 0, f"{name}: {err[-2000:]}"
-        asm = out.read_text()
+        asm[name] = out.read_text()
+    return asm
+
+
+def test_lds_dma_wait_states(compiled):
+    report, copies, kwaits = [], 0, 0
+    for name, asm in compiled.items():
         copies += asm.count("global_load_lds_dwordx4")
         report += [f"{name}: {h}" for h in hazards(asm)]
         n, found = kload_findings(asm)
@@ -188,3 +204,49 @@ def test_lds_dma_wait_states(tmp_path):
     assert copies > 0, "no LDS DMA copies found: the checker is looking at the wrong code"
     assert kwaits > 0, "no K-load waits found: the checker is looking at the wrong code"
     assert not report, "\n".join(report)
+
+
+def kernel_resources(asm: str) -> dict[str, tuple[int, int]]:
+    """Kernel symbol -> (VGPRs, AGPRs included, and scratch bytes per lane)
+    from the code object's kernel descriptors."""
+    out = {}
+    for m in re.finditer(r"\.amdhsa_kernel (\S+)(.*?)\.end_amdhsa_kernel", asm, re.S):
+        body = m.group(2)
+        vgpr = int(re.search(r"\.amdhsa_next_free_vgpr (\d+)", body).group(1))
+        scratch = int(re.search(r"\.amdhsa_private_segment_fixed_size (\d+)", body).group(1))
+        out[m.group(1)] = (vgpr, scratch)
+    return out
+
+
+# Register budgets the performance depends on: (symbol pattern, VGPR limit,
+# why). Every kernel listed must also run without scratch.
+BUDGETS = [
+    # the selective scan's output kernel: five resident work-groups per CU
+    # (five waves per SIMD) is what config 4's 1280 work-groups need
+    (r"selective_scan_out", 96, "five waves per SIMD"),
+    # the production prefill (two LDS stages): two work-groups per CU
+    (r"attn_fwd_d128INS_7Bf16TagELb1ELi2ELb0E", 256, "two waves per SIMD"),
+    # the decode partial kernels: a scratch reload's wait would retire the
+    # copies in flight
+    (r"decode_partial_ring", 512, "no scratch"),
+]
+
+
+def test_kernel_register_budgets(compiled):
+    res = {}
+    for asm in compiled.values():
+        res.update(kernel_resources(asm))
+    report = []
+    for pat, limit, why in BUDGETS:
+        hits = {k: v for k, v in res.items() if re.search(pat, k)}
+        assert hits, f"no kernel matches {pat}: the check is looking at the wrong code"
+        for k, (vgpr, scratch) in hits.items():
+            if vgpr > limit or scratch:
+                report.append(f"{k}: {vgpr} VGPRs (limit {limit}, {why}), {scratch} B scratch")
+    assert not report, "\n".join(report)
+
+
+def test_kernel_resources_parser():
+    asm = ("\t.amdhsa_kernel _Zfoo\n\t\t.amdhsa_private_segment_fixed_size 8\n"
+           "\t\t.amdhsa_next_free_vgpr 97\n\t.end_amdhsa_kernel\n")
+    assert kernel_resources(asm) == {"_Zfoo": (97, 8)}
