@@ -122,27 +122,26 @@ __device__ inline float *chunk_scratch(const ScanArgs &a, int b, int d, int k) {
   return reinterpret_cast<float *>(a.y + ((int64_t)b * a.Dm + d) * a.L + chunk_start(a, k));
 }
 
-__device__ inline float lo_bf16(uint32_t p) { return __uint_as_float(p << 16); }
-__device__ inline float hi_bf16(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
 
-__device__ inline float softplus_fast(float v) {
-  // log(1 + e^v) = ln2 * log2(1 + 2^(v log2 e)); torch returns v above 20
-  return v > 20.0f ? v : 0.69314718055994531f * __builtin_amdgcn_logf(1.0f + fast_exp2(v * kLog2e));
-}
 
 __device__ inline float silu_fast(float z) {
   return z * __builtin_amdgcn_rcpf(1.0f + fast_exp2(-z * kLog2e));
 }
 
+// softplus's linear branch (torch: delta_raw + bias above 20), in log2 units
+constexpr float kSoftplusLinear2 = 20.0f * kLog2e;
+
 // The state pass of the chunked path: the recurrence alone, from x = 0, over
 // every chunk but the last; leaves the chunk's end state and delta sum at
 // the start of its own y segment.
+template <bool SOFTPLUS>
 __global__ __launch_bounds__(NT) void selective_scan_state(ScanArgs a) {
-  // (delta, delta*u) for two steps per float4, and B of one state for two
-  // steps; one float4 of padding per row keeps the 16 rows read together in
-  // distinct banks
-  __shared__ float4 pre[SCH][TP + 1];
-  __shared__ float2 bsh[ST][TP + 2];
+  // (delta log2 e, delta u) for two steps per float4, and B of one state for
+  // two steps, double-buffered by chunk parity (one barrier per chunk); one
+  // float4 of padding per row keeps the 16 rows read together in distinct
+  // banks
+  __shared__ float4 pre[2][SCH][TP + 1];
+  __shared__ float2 bsh[2][ST][TP + 2];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = tid >> 6;
@@ -157,13 +156,13 @@ __global__ __launch_bounds__(NT) void selective_scan_state(ScanArgs a) {
   const int tb = chunk_start(a, kc);
   const int te = chunk_start(a, kc + 1);
 
-  // scan identity: channel c, state n
+  // scan identity: channel c, state n; the decay is 2^(delta log2 e * A)
   const int c = lane & 15, r = lane >> 4;
   const int n = 4 * w + r;
   const bool cok = d0 + c < a.Dm;
-  const float A2 = cok ? a.A[(int64_t)(d0 + c) * ST + n] * kLog2e : 0.0f;
+  const float Ac = cok ? a.A[(int64_t)(d0 + c) * ST + n] : 0.0f;
   float x = 0.0f;
-  float dsum = 0.0f;  // this thread's share of the chunk's delta sum
+  float dsum = 0.0f;  // this thread's share of the chunk's delta log2 e
 
   // stage identity: channel sc, steps 2 sp and 2 sp + 1 of a chunk; B
   // identity: state tid / 16, same step pair
@@ -171,57 +170,59 @@ __global__ __launch_bounds__(NT) void selective_scan_state(ScanArgs a) {
   const int sd = d0 + sc;
   const bool sok = sd < a.Dm;
   const int bn = tid / TP;
-  const int64_t srow = ((int64_t)b * a.Dm + (sok ? sd : 0)) * a.L;
+  // rows past the last channel read the block's first row (unused)
+  const int64_t srow = ((int64_t)b * a.Dm + (sok ? sd : d0)) * a.L;
   const int64_t bcrow = ((int64_t)b * ST + bn) * a.L;
-  const float bias = (sok && a.bias) ? a.bias[sd] : 0.0f;
+  const float bias2 = (sok && a.bias) ? a.bias[sd] * kLog2e : 0.0f;
 
-  // a non-last chunk lies inside the sequence and the path needs even L
-  // and 4-byte aligned rows, so every step pair is one dword
-  uint32_t pu = 0, pdr = 0, pB = 0;
+  // every chunk of this pass lies inside the sequence, and so does the step
+  // pair after it (the last chunk follows), so the loads need no guard; the
+  // path needs even L and 4-byte aligned rows, so a step pair is one dword
+  uint32_t pu, pdr, pB;
   auto fetch = [&](int t0) {
     const int t = t0 + 2 * sp;
-    if (sok) {
-      pu = *(const uint32_t *)(a.u + srow + t);
-      pdr = *(const uint32_t *)(a.dr + srow + t);
-    }
+    pu = *(const uint32_t *)(a.u + srow + t);
+    pdr = *(const uint32_t *)(a.dr + srow + t);
     pB = *(const uint32_t *)(a.Bm + bcrow + t);
   };
 
   fetch(tb);
-  for (int t0 = tb; t0 < te; t0 += TT) {
+  for (int t0 = tb, par = 0; t0 < te; t0 += TT, par ^= 1) {
     {
-      const float uu[2] = {lo_bf16(pu), hi_bf16(pu)};
-      const float dl[2] = {lo_bf16(pdr), hi_bf16(pdr)};
+      const float uu[2] = {__uint_as_float(pu << 16), __uint_as_float(pu & 0xffff0000u)};
+      const float dr[2] = {__uint_as_float(pdr << 16), __uint_as_float(pdr & 0xffff0000u)};
       float4 pv;
       float *pf = reinterpret_cast<float *>(&pv);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const float v = dl[i] + bias;
-        const float delta = a.softplus ? softplus_fast(v) : v;
-        pf[2 * i] = delta;
-        pf[2 * i + 1] = delta * uu[i];
-        dsum += delta;
+        // (delta_raw + bias) log2 e, and delta log2 e = log2(1 + 2^that)
+        // below the linear branch
+        const float v2 = fmaf(dr[i], kLog2e, bias2);
+        const float d2 =
+            SOFTPLUS && !(v2 > kSoftplusLinear2) ? __builtin_amdgcn_logf(1.0f + fast_exp2(v2)) : v2;
+        pf[2 * i] = d2;
+        pf[2 * i + 1] = d2 * (uu[i] * kLn2);
+        dsum += d2;
       }
-      pre[sc][sp] = pv;
-      bsh[bn][sp] = make_float2(lo_bf16(pB), hi_bf16(pB));
+      pre[par][sc][sp] = pv;
+      bsh[par][bn][sp] = make_float2(__uint_as_float(pB << 16), __uint_as_float(pB & 0xffff0000u));
     }
-    if (t0 + TT < te) fetch(t0 + TT);
+    fetch(t0 + TT);
+    // this chunk's buffers are next written two chunks on, behind the next
+    // chunk's barrier, which every wave reaches after its reads of this one
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < TP; ++j) {
-      const float4 pd = pre[c][j];
-      const float2 q = bsh[n][j];
-      x = fmaf(fast_exp2(pd.x * A2), x, pd.y * q.x);
-      x = fmaf(fast_exp2(pd.z * A2), x, pd.w * q.y);
+      const float4 pd = pre[par][c][j];
+      const float2 q = bsh[par][n][j];
+      x = fmaf(fast_exp2(pd.x * Ac), x, pd.y * q.x);
+      x = fmaf(fast_exp2(pd.z * Ac), x, pd.w * q.y);
     }
-    // pre / bsh are rewritten by the next stage only after every wave is
-    // done with them
-    __syncthreads();
   }
   if (cok) chunk_scratch(a, b, d0 + c, kc)[n] = x;
 #pragma unroll
   for (int off = 1; off < TP; off <<= 1) dsum += __shfl_xor(dsum, off, 64);
-  if (sok && sp == 0) chunk_scratch(a, b, sd, kc)[ST] = dsum;
+  if (sok && sp == 0) chunk_scratch(a, b, sd, kc)[ST] = dsum * kLn2;  // natural units
 }
 
 // Cross-lane exchange through LDS inside one wave: the wave's LDS
@@ -276,8 +277,6 @@ __device__ inline __amdgpu_buffer_rsrc_t byte_range(const void *base, uint32_t b
                                            0x00020000);
 }
 
-// softplus's linear branch (torch: delta_raw + bias above 20), in log2 units
-constexpr float kSoftplusLinear2 = 20.0f * kLog2e;
 // a byte offset past every output resource (at most 16 rows x 2 x 2^26
 // bytes): a store there is dropped by the range check
 constexpr uint32_t kDropped = 0x80000000u;
@@ -640,8 +639,11 @@ hipError_t launch_selective_scan(const ScanLaunch &L, hipStream_t s) {
     out(std::integral_constant<int, kScanFull>{}, (unsigned)groups);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL(selective_scan_state, dim3((unsigned)(groups * (a.nch - 1))), dim3(NT), 0,
-                     s, a);
+  const dim3 sgrid((unsigned)(groups * (a.nch - 1)));
+  if (L.delta_softplus)
+    hipLaunchKernelGGL(selective_scan_state<true>, sgrid, dim3(NT), 0, s, a);
+  else
+    hipLaunchKernelGGL(selective_scan_state<false>, sgrid, dim3(NT), 0, s, a);
   const int64_t lanes = L.batch * L.dim * ST;
   // a long chain of chunks: one wave per (batch, channel, state); up to 64
   // summaries the per-lane walk measured as fast or faster
