@@ -102,7 +102,7 @@ def _chunked(b, d, L):
 
 @pytest.mark.parametrize("b,d,L,bias,gate", [
     (1, 64, 65536, True, True),    # 4 channel blocks over a long sequence: 320 chunks
-    (1, 20, 9000, True, True),     # 140 chunks: the wave carry's two full passes and a part
+    (2, 20, 9000, True, True),     # 140 chunks: the wave carry's two full passes and a part
     (1, 16, 4096, False, True),    # one channel block, 64 chunks of 64 steps
     (2, 48, 1000, True, False),    # ragged channel block, chunks of 96, 64 and 72 steps
     (1, 8, 130, True, True),       # two chunks, the second 66 steps
