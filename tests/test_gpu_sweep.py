@@ -17,7 +17,9 @@ checks the result against the CPU oracle at the contract's tolerances:
 * selective scan (neptune_selective_scan_fwd): batch 1-3, ragged channel
   counts, lengths 1-1500 (odd ones take the single pass, even ones of two
   64-step chunks or more the chunked path when the channels leave the GPU
-  unfilled), with or without z, D and delta_bias, softplus on or off.
+  unfilled), with or without z, D and delta_bias, softplus on or off; and
+  eight long few-channel cases (lengths 2048-24000, 1-47 channels), whose
+  chains of more than 64 chunks take the wave-parallel carry.
 """
 
 import numpy as np
@@ -218,9 +220,27 @@ def _scan_case(i):
                 softplus=bool(rng.integers(0, 4)), seed=4000 + i)
 
 
+def _scan_long_case(i):
+    """Few channels over long even sequences: the chunked path with chains of
+    more than 64 chunks (the wave-parallel carry)."""
+    rng = np.random.default_rng(9000 + i)
+    L = int(rng.integers(1024, 12000)) * 2
+    return dict(b=int(rng.integers(1, 3)), d=int(rng.integers(1, 48)), L=L,
+                gate=bool(rng.integers(0, 2)), with_d=bool(rng.integers(0, 2)),
+                bias=bool(rng.integers(0, 2)), softplus=bool(rng.integers(0, 4)), seed=9000 + i)
+
+
 @pytest.mark.parametrize("i", range(60))
 def test_scan_sweep(ops, i):
-    c = _scan_case(i)
+    _scan_sweep_case(ops, _scan_case(i))
+
+
+@pytest.mark.parametrize("i", range(8))
+def test_scan_sweep_long(ops, i):
+    _scan_sweep_case(ops, _scan_long_case(i))
+
+
+def _scan_sweep_case(ops, c):
     _log(f"case: scan sweep {c}")
     b, d, L, n = c["b"], c["d"], c["L"], 16
     u, z = randn((b, d, L), seed=c["seed"]), randn((b, d, L), seed=c["seed"] + 1)
