@@ -144,7 +144,8 @@ typedef struct neptune_paged_kv_desc {
  * is carried in fp32 from x = 0. y must not overlap any input: the call
  * writes y while it still reads later steps, and for few channels over a
  * long sequence it keeps per-chunk state in y before the outputs overwrite
- * it (no workspace). Supported: d_state 16 and seq_len below 2^26
+ * it (no workspace); a y that shares a byte with an input is
+ * NEPTUNE_ERR_INVALID_ARGUMENT. Supported: d_state 16 and seq_len below 2^26
  * (NEPTUNE_ERR_UNSUPPORTED otherwise). */
 typedef struct neptune_scan_desc {
   int64_t batch, dim, seq_len, d_state;

@@ -91,6 +91,12 @@ void decode_layout(const neptune_decode_desc *d, int64_t *splits, int64_t *chunk
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// whether the byte ranges [a, a + na) and [b, b + nb) share a byte
+bool overlaps(const void *a, size_t na, const void *b, size_t nb) {
+  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+  return na && nb && x < y + nb && y < x + na;
+}
+
 neptune_status decode_check(const neptune_decode_desc *d) {
   if (!d) return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode: desc is NULL");
   if (d->batch <= 0 || d->heads_q <= 0 || d->heads_kv <= 0 || d->seq_kv <= 0 ||
@@ -416,6 +422,23 @@ neptune_status neptune_selective_scan_fwd(const neptune_scan_desc *d, const void
   L.delta_softplus = d->delta_softplus ? 1 : 0;
   const char *why = "";
   if (!scan_supported(L, &why)) return fail(NEPTUNE_ERR_UNSUPPORTED, "selective_scan: %s", why);
+  // y is written while later steps of the inputs are still being read, and
+  // holds per-chunk state before the outputs: it may share no input byte
+  // (sizes are below 2^63 once scan_supported has passed)
+  const size_t rows = (size_t)d->batch * (size_t)d->seq_len * 2;
+  const size_t act = rows * (size_t)d->dim, bc = rows * (size_t)d->d_state;
+  const struct { const void *p; size_t n; const char *name; } in[] = {
+      {u, act, "u"},
+      {delta_raw, act, "delta"},
+      {z, z ? act : 0, "z"},
+      {B, bc, "B"},
+      {C, bc, "C"},
+      {A, (size_t)d->dim * (size_t)d->d_state * 4, "A"},
+      {D, D ? (size_t)d->dim * 4 : 0, "D"},
+      {delta_bias, delta_bias ? (size_t)d->dim * 4 : 0, "delta_bias"}};
+  for (const auto &t : in)
+    if (overlaps(y, act, t.p, t.n))
+      return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "selective_scan: y overlaps %s", t.name);
   neptune_status st = device_ready();
   if (st != NEPTUNE_OK) return st;
   return hip_result(launch_selective_scan(L, (hipStream_t)stream), "selective_scan launch");

@@ -181,6 +181,12 @@ int run_validate() {
   expect(neptune_selective_scan_fwd(&s, fake, fake, (const float *)fake, fake, fake, nullptr,
                                     nullptr, nullptr, fake, nullptr) ==
              NEPTUNE_ERR_INVALID_ARGUMENT, "scan: seq_len 0");
+  s.seq_len = 128;
+  expect(neptune_selective_scan_fwd(&s, fake, fake, (const float *)fake, fake, fake, nullptr,
+                                    nullptr, nullptr, fake, nullptr) ==
+             NEPTUNE_ERR_INVALID_ARGUMENT &&
+             std::string(neptune_last_error()) == "selective_scan: y overlaps u",
+         "scan: y overlapping u");
 
   const int devices = neptune_device_count();
   if (devices == 0) {

@@ -380,7 +380,50 @@ def test_quantize_and_scan_validation(lib):
     assert b"seq_len below 2^26" in lib.neptune_last_error()
     if lib.neptune_device_count() == 0:
         just_under = _abi.ScanDesc(1, 16, (1 << 26) - 2, 16, _abi.DTYPE_BF16, 1)
-        assert s(ctypes.byref(just_under), *([FAKE] * 9), None) == _abi.ERR_NO_DEVICE
+        apart = [FAKE + (i << 32) for i in range(9)]  # 4 GiB apart: no overlap
+        assert s(ctypes.byref(just_under), *apart, None) == _abi.ERR_NO_DEVICE
+
+
+def _scan_pointers(**moved):
+    """Fake addresses of u, delta, A, B, C, D, z, delta_bias, y, 1 MiB apart
+    (no overlap for the 1x64x128 desc below), with `moved` ones replaced."""
+    names = ("u", "delta", "A", "B", "C", "D", "z", "delta_bias", "y")
+    base = {n: FAKE + (i << 20) for i, n in enumerate(names)}
+    base.update(moved)
+    return [base[n] for n in names]
+
+
+@pytest.mark.parametrize("moved, culprit", [
+    ({"y": FAKE}, b"u"),                                   # y is u
+    ({"y": FAKE + (1 << 20) + 16 * 1024 - 2}, b"delta"),   # y's first element is delta's last
+    ({"y": FAKE + (3 << 20) - 16 * 1024 + 2}, b"B"),       # y's tail runs into B
+    ({"y": FAKE + (5 << 20) + 200}, b"D"),                 # D inside y
+    ({"z": FAKE + (8 << 20) + 4096}, b"z"),                # z inside y
+    ({"delta_bias": FAKE + (8 << 20)}, b"delta_bias"),
+])
+def test_scan_rejects_y_overlapping_an_input(lib, moved, culprit):
+    """y is written while later steps are read and holds per-chunk state, so
+    a y that shares any byte with an input is INVALID_ARGUMENT, checked before
+    any device work."""
+    d = _abi.ScanDesc(1, 64, 128, 16, _abi.DTYPE_BF16, 1)  # u, delta, z, y 16 KiB; B, C 4 KiB
+    s = lib.neptune_selective_scan_fwd
+    assert s(ctypes.byref(d), *_scan_pointers(**moved), None) == _abi.ERR_INVALID_ARGUMENT
+    assert lib.neptune_last_error() == b"selective_scan: y overlaps " + culprit
+
+
+def test_scan_accepts_adjacent_and_null_optional_inputs(lib):
+    """Ranges that touch but share no byte, and NULL D, z and delta_bias,
+    pass the overlap check (NO_DEVICE on a host without a GPU)."""
+    if lib.neptune_device_count() > 0:
+        pytest.skip("a HIP device is visible: a valid request would launch on fake pointers")
+    d = _abi.ScanDesc(1, 64, 128, 16, _abi.DTYPE_BF16, 1)
+    s = lib.neptune_selective_scan_fwd
+    ptr = _scan_pointers(y=FAKE + 16 * 1024)  # y starts where u ends
+    assert s(ctypes.byref(d), *ptr, None) == _abi.ERR_NO_DEVICE
+    ptr = _scan_pointers(y=FAKE + (3 << 20) - 16 * 1024)  # y ends where B starts
+    assert s(ctypes.byref(d), *ptr, None) == _abi.ERR_NO_DEVICE
+    ptr = _scan_pointers(D=None, z=None, delta_bias=None, y=FAKE + (5 << 20))
+    assert s(ctypes.byref(d), *ptr, None) == _abi.ERR_NO_DEVICE
 
 
 def test_no_device_path(lib):
