@@ -92,6 +92,63 @@ def test_config4_full_shape(ops):
     _check(y.cpu(), ins, chan)
 
 
+# config 4 (the single pass) and a few channels over a long sequence (the
+# sequence-parallel path: 320 chunks, the wave-parallel carry)
+FULL_SHAPES = [(4, 5120, 2048), (1, 64, 65536)]
+
+
+@pytest.mark.parametrize("shape", FULL_SHAPES, ids=["config4", "b1d64L65536"])
+def test_scan_full_size_linear_in_u(ops, shape):
+    """Every channel: y(2u) = 2 y(u) bit for bit. u enters the
+    recurrence, the skip term and nothing else, each time through products
+    and sums that doubling commutes with exactly in fp32 and in the bf16
+    rounding of y (no value here is near the subnormal range), so any
+    channel, state or step whose mapping differs between the two calls, or
+    an input read out of place, breaks the equality."""
+    _log(f"case: scan linear in u, shape {shape}")
+    u, dr, A, Bm, Cm, D, z, bias = scan_inputs(*shape, seed=300)
+    dev = [t.cuda() if t is not None else None for t in (u, dr, A, Bm, Cm, D, z, bias)]
+    y1 = ops.selective_scan(*dev)
+    dev[0] = (2 * u).cuda()
+    y2 = ops.selective_scan(*dev)
+    torch.cuda.synchronize()
+    y1, y2 = y1.cpu(), y2.cpu()
+    assert torch.isfinite(y1.float()).all()
+    diff = (bits(y2) != bits(2 * y1))
+    assert not diff.any(), (np.argwhere(diff)[:5], int(diff.sum()))
+
+
+@pytest.mark.parametrize("shape", FULL_SHAPES, ids=["config4", "b1d64L65536"])
+@pytest.mark.parametrize("case", ["B zero", "C zero", "delta zero"])
+def test_scan_full_size_skip_term_only(ops, case, shape):
+    """Every channel, where the state term vanishes: with B = 0
+    the state stays 0, with C = 0 it is not read, and with delta = 0 (no
+    softplus, no bias) the state gains nothing. Then y = D u silu(z), within
+    one bf16 ulp of that product in fp32 (the kernel forms D u as
+    (D log2 e)(u ln2) and silu through the hardware reciprocal)."""
+    _log(f"case: scan skip term only, {case}, shape {shape}")
+    u, dr, A, Bm, Cm, D, z, bias = scan_inputs(*shape, seed=400)
+    softplus = True
+    if case == "B zero":
+        Bm = torch.zeros_like(Bm)
+    elif case == "C zero":
+        Cm = torch.zeros_like(Cm)
+    else:
+        dr, bias, softplus = torch.zeros_like(dr), None, False
+    y = ops.selective_scan(*(t.cuda() if t is not None else None
+                             for t in (u, dr, A, Bm, Cm, D, z, bias)),
+                           delta_softplus=softplus)
+    torch.cuda.synchronize()
+    zf = z.float()
+    want = D.view(1, -1, 1) * u.float() * (zf * torch.sigmoid(zf))
+    got = y.cpu().float()
+    # one bf16 ulp of the result (8 significant bits), plus the smallest
+    # normal step for results near 0
+    ulp = torch.exp2(torch.floor(torch.log2(want.abs().clamp_min(2.0 ** -120))) - 7)
+    err = (got - want).abs()
+    assert (err <= ulp).all(), (float(err.max()), int((err > ulp).sum()))
+
+
 def _chunked(b, d, L):
     """Whether the library takes the sequence-parallel path for this shape
     (the rule of scan_chunking in scan.hip: fewer than 1024 work-groups of 16
