@@ -170,6 +170,25 @@ def test_config2_full_shape(ops):
         assert max_abs(to_f32(lse[sl]), ref_lse) <= TOL_LSE_ABS, (b, h)
 
 
+def test_config2_full_shape_linear_in_v(ops):
+    """Config 2 at full size, every head and row: O(2V) = 2 O(V) bit for bit
+    and the same LSE. The scores, maxima, rescale decisions and P do not
+    depend on V; doubling V doubles every P.V product and fp32 partial sum
+    exactly, and commutes with the division by l and the bf16 rounding, so
+    any output row whose work differs between the two calls breaks it."""
+    _log("case: config2 linear in V")
+    shape = (4, 32, 4096, 128)
+    g = torch.Generator(device="cuda").manual_seed(21)
+    q, k, v = (torch.randn(shape, device="cuda", generator=g).mul_(0.5).to(torch.bfloat16)
+               for _ in range(3))
+    o1, lse1 = ops.attention(q, k, v, causal=True, return_lse=True)
+    o2, lse2 = ops.attention(q, k, 2 * v, causal=True, return_lse=True)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(o1).all())
+    assert torch.equal(lse1, lse2)
+    assert torch.equal(o2, 2 * o1)
+
+
 def test_q_zero_gives_prefix_mean(ops):
     """Q = 0: uniform weights, so row i is the mean of V[0..i] (causal)."""
     _log("case: q zero prefix mean")

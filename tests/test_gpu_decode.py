@@ -200,6 +200,38 @@ def test_config5_full_shape(ops):
         assert max_abs(got, ref) <= 6e-2 * np.abs(ref).max()
 
 
+@pytest.mark.parametrize("fp8", [False, True], ids=["config3", "config5"])
+def test_full_shape_linear_in_v(ops, fp8):
+    """Configs 3 and 5 at full size, every (batch, query head): O(2V) = 2 O(V)
+    bit for bit and the same LSE. The split maxima, sums and combine weights
+    do not depend on V, and doubling V doubles every product and partial sum
+    exactly. With fp8 KV the quantiser keeps the codes of 2V and doubles
+    their scales (amax / 448 commutes with doubling), checked first."""
+    _log(f"case: decode linear in V, fp8={fp8}")
+    g = torch.Generator(device="cuda").manual_seed(31)
+    q = torch.randn((16, 32, 128), device="cuda", generator=g).to(torch.bfloat16)
+    k = torch.randn((16, 8, 32768, 128), device="cuda", generator=g).to(torch.bfloat16)
+    v = torch.randn((16, 8, 32768, 128), device="cuda", generator=g).to(torch.bfloat16)
+    if fp8:
+        kc, ks = ops.kv_quantize_fp8(k)
+        vc, vs = ops.kv_quantize_fp8(v)
+        vc2, vs2 = ops.kv_quantize_fp8(2 * v)
+        del k, v
+        assert torch.equal(vc2, vc)
+        assert torch.equal(vs2, 2 * vs)
+        o1, lse1 = ops.decode_splitk(q, kc, vc, k_scale=ks, v_scale=vs, num_splits=16,
+                                     return_lse=True)
+        o2, lse2 = ops.decode_splitk(q, kc, vc2, k_scale=ks, v_scale=vs2, num_splits=16,
+                                     return_lse=True)
+    else:
+        o1, lse1 = ops.decode_splitk(q, k, v, num_splits=16, return_lse=True)
+        o2, lse2 = ops.decode_splitk(q, k, 2 * v, num_splits=16, return_lse=True)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(o1).all())
+    assert torch.equal(lse1, lse2)
+    assert torch.equal(o2, 2 * o1)
+
+
 def test_workspace_too_small(ops):
     from neptune_hip import NeptuneWorkspaceTooSmall
     q = torch.zeros((1, 4, 128), dtype=torch.bfloat16, device="cuda")
