@@ -78,6 +78,40 @@ def test_paged_equals_contiguous_bitwise(ops, token_major):
     assert torch.equal(lse, lse_ref)
 
 
+@pytest.mark.parametrize("token_major", [False, True])
+def test_paged_equals_contiguous_config3_full_size(ops, token_major):
+    """Config 3 at full size (B=16 Hq=32 Hkv=8 L=32768 D=128, 16 splits) in
+    64-token pages, shuffled over the pool on the device: every (batch,
+    query head) bit-identical to the contiguous kernel, output and LSE."""
+    _log(f"case: paged == contiguous at config 3, token_major={token_major}")
+    B, Hq, Hk, L, D, ps = 16, 32, 8, 32768, 128, 64
+    per = L // ps
+    g = torch.Generator(device="cuda").manual_seed(41)
+    q = torch.randn((B, Hq, D), device="cuda", generator=g).to(torch.bfloat16)
+    k = torch.randn((B, Hk, L, D), device="cuda", generator=g).to(torch.bfloat16)
+    v = torch.randn((B, Hk, L, D), device="cuda", generator=g).to(torch.bfloat16)
+    ids = torch.randperm(B * per, device="cuda", generator=g)
+    table = ids.view(B, per).to(torch.int32)
+
+    def pool_of(kv):
+        blocks = kv.view(B, Hk, per, ps, D).permute(0, 2, 1, 3, 4)  # [B, per, Hk, ps, D]
+        if token_major:
+            blocks = blocks.transpose(2, 3)                          # [B, per, ps, Hk, D]
+        pool = torch.empty((B * per,) + tuple(blocks.shape[2:]), dtype=kv.dtype, device="cuda")
+        pool[ids] = blocks.reshape((B * per,) + tuple(blocks.shape[2:]))
+        return pool.permute(0, 2, 1, 3) if token_major else pool
+
+    kp, vp = pool_of(k), pool_of(v)
+    lens = torch.full((B,), L, dtype=torch.int32, device="cuda")
+    o_ref, lse_ref = ops.decode_splitk(q, k, v, num_splits=16, return_lse=True)
+    o, lse = ops.decode_paged(q, kp, vp, table, lens, max_seq_len=L, num_splits=16,
+                              return_lse=True)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(o_ref).all())
+    assert torch.equal(o.view(torch.int16), o_ref.view(torch.int16))
+    assert torch.equal(lse, lse_ref)
+
+
 def test_paged_ragged_lengths_match_oracle(ops):
     _log("case: paged ragged lengths")
     B, Hq, Hk, L, D, ps = 3, 8, 2, 1000, 128, 128
