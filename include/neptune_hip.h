@@ -187,8 +187,9 @@ NEPTUNE_API neptune_status neptune_decode_splitk(const neptune_decode_desc *desc
  * split partials go to a static device scratch of 16 MiB that each GPU
  * holds until the process ends (520 bytes per batch x heads_q x split row:
  * config 3's 16 x 32 x 16 rows use 4.3 MB); a request that needs more
- * returns NEPTUNE_ERR_WORKSPACE_TOO_SMALL. Every call on one GPU shares that
- * scratch: calls that overlap on one GPU (concurrent streams, or threads
+ * returns NEPTUNE_ERR_WORKSPACE_TOO_SMALL. The kernels use the scratch of the
+ * device that owns `stream` (the current device for the null stream). Every
+ * call on one GPU shares that scratch: calls that overlap on one GPU (concurrent streams, or threads
  * enqueueing at once) race on it and must be ordered by the caller. The
  * results equal neptune_decode_splitk's bit for bit. */
 NEPTUNE_API neptune_status neptune_decode_splitk_noalloc(const neptune_decode_desc *desc,

@@ -272,7 +272,7 @@ neptune_status decode_run(const neptune_decode_desc *d, const neptune_paged_kv_d
   neptune_status st = device_ready();
   if (st != NEPTUNE_OK) return st;
   if (scratch) {
-    st = hip_result(decode_scratch(&workspace), "decode_noalloc: scratch address");
+    st = hip_result(decode_scratch((hipStream_t)stream, &workspace), "decode_noalloc: scratch address");
     if (st != NEPTUNE_OK) return st;
   }
   const size_t rows = (size_t)d->batch * d->heads_q * splits;

@@ -977,18 +977,30 @@ static __device__ __align__(256) unsigned char scratch[neptune::kDecodeScratchBy
 
 namespace neptune {
 
-hipError_t decode_scratch(void **ptr) {
+// The scratch address on the device that owns stream s (the null and
+// per-thread streams: the current device), resolved once per device with
+// that device current.
+hipError_t decode_scratch(hipStream_t s, void **ptr) {
   constexpr int kMaxDevices = 64;
   static std::mutex mu;
   static void *addr[kMaxDevices] = {};
   int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
+  hipError_t e = (s == nullptr || s == hipStreamPerThread) ? hipGetDevice(&dev)
+                                                           : hipStreamGetDevice(s, &dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(mu);
   if (!addr[dev]) {
+    int cur = -1;
+    e = hipGetDevice(&cur);
+    if (e != hipSuccess) return e;
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
     void *p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) {
+      const hipError_t back = hipSetDevice(cur);
+      if (e == hipSuccess) e = back;
+    }
     if (e != hipSuccess) return e;
     addr[dev] = p;
   }

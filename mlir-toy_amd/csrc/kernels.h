@@ -57,9 +57,10 @@ struct ScanLaunch {
 // (the split partials of one call: 520 bytes per (batch, query head, split)).
 constexpr size_t kDecodeScratchBytes = size_t(16) << 20;
 
-// Device address of that scratch on the current device, resolved once per
-// device by hipGetSymbolAddress and kept; hipSuccess or the HIP error.
-hipError_t decode_scratch(void **ptr);
+// Device address of that scratch on the device that owns stream s (the
+// current device for the null stream), resolved once per device by
+// hipGetSymbolAddress and kept; hipSuccess or the HIP error.
+hipError_t decode_scratch(hipStream_t s, void **ptr);
 
 // Each returns hipSuccess or the launch error. Shapes the kernels do not
 // cover are rejected by the ABI layer before these are called.

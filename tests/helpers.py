@@ -12,6 +12,31 @@ TOL_F32_REL = 1e-5      # fp32: max|a-b| <= 1e-5 * max|ref|
 TOL_BF16_ABS = 2e-2     # bf16: max-abs
 TOL_FP8_ABS = 6e-2      # fp8 KV: max-abs
 TOL_LSE_ABS = 1e-3      # logsumexp (fp32 output)
+# Decode outputs of N(0,1) data are ~0.03, where the max-abs bounds above
+# cannot fail, so decode checks also hold each sequence to a bound relative
+# to its own largest reference output:
+TOL_BF16_REL = 2e-2     # kernel against the oracle on the same K/V (bf16 or fp8 codes)
+TOL_FP8_REL = 6e-2      # fp8 KV end to end, against the oracle on the bf16 K/V
+
+
+def rel_err_rows(got: np.ndarray, ref: np.ndarray) -> float:
+    """Worst over the leading index (a decode batch's sequences) of
+    max|got - ref| / max|ref| on that slice. A slice whose reference is all
+    zero (an empty sequence) must match exactly: it gives inf otherwise."""
+    worst = 0.0
+    for g, r in zip(got, ref):
+        err = max_abs(np.asarray(g), np.asarray(r))
+        top = float(np.max(np.abs(r))) if np.size(r) else 0.0
+        worst = max(worst, err / top if top > 0 else (0.0 if err == 0 else np.inf))
+    return worst
+
+
+def assert_rel_rows(got: np.ndarray, ref: np.ndarray, tol: float, what: str = "") -> float:
+    """rel_err_rows(got, ref) <= tol; prints and returns the measured ratio."""
+    r = rel_err_rows(got, ref)
+    print(f"  rel err {what}: {r:.3e} (bound {tol:g})", flush=True)
+    assert r <= tol, (what, r, tol)
+    return r
 
 
 def bits(t: torch.Tensor) -> np.ndarray:

@@ -19,7 +19,8 @@ import pytest
 import torch
 
 import oracle
-from helpers import TOL_BF16_ABS, TOL_FP8_ABS, TOL_LSE_ABS, bits, randn, to_f32
+from helpers import (TOL_BF16_ABS, TOL_BF16_REL, TOL_FP8_ABS, TOL_LSE_ABS, assert_rel_rows, bits,
+                     randn, to_f32)
 
 pytestmark = pytest.mark.gpu
 
@@ -126,7 +127,9 @@ def test_paged_ragged_lengths_match_oracle(ops):
     torch.cuda.synchronize()
     to, tl = oracle.decode_paged(bits(q), bits(kp), bits(vp), table.cpu().numpy(),
                                  np.array(lens, np.int32), max_seq_len=L, num_splits=4)
-    assert np.abs(to_f32(o) - oracle.decode(to, oracle.BF16)).max() <= TOL_BF16_ABS
+    ref_all = oracle.decode(to, oracle.BF16)
+    assert np.abs(to_f32(o) - ref_all).max() <= TOL_BF16_ABS
+    assert_rel_rows(to_f32(o), ref_all, TOL_BF16_REL, "paged ragged vs twin")
     assert np.abs(to_f32(lse) - tl).max() <= TOL_LSE_ABS
     for b, n in enumerate(lens):
         ro, rl, _ = oracle.decode_splitk(bits(q[b:b + 1]), bits(k[b:b + 1, :, :n]),
@@ -157,7 +160,9 @@ def test_paged_empty_sequence_and_bad_table(ops):
     assert torch.isfinite(o2.float()).all()
     to, _ = oracle.decode_paged(bits(q), bits(kp), bits(vp), bad.cpu().numpy(),
                                 lens.cpu().numpy(), max_seq_len=L)
-    assert np.abs(to_f32(o2) - oracle.decode(to, oracle.BF16)).max() <= TOL_BF16_ABS
+    ref2 = oracle.decode(to, oracle.BF16)
+    assert np.abs(to_f32(o2) - ref2).max() <= TOL_BF16_ABS
+    assert_rel_rows(to_f32(o2), ref2, TOL_BF16_REL, "paged bad table vs twin")
 
 
 def page_scales(scales, table, npages, seed):
@@ -201,7 +206,9 @@ def test_paged_fp8_equals_contiguous_bitwise(ops, token_major):
                                  table.cpu().numpy(), lens.cpu().numpy(), max_seq_len=L,
                                  num_splits=splits, k_scales=kps.cpu().numpy(),
                                  v_scales=vps.cpu().numpy())
-    assert np.abs(to_f32(o) - oracle.decode(to, oracle.BF16)).max() <= TOL_FP8_ABS
+    ref = oracle.decode(to, oracle.BF16)
+    assert np.abs(to_f32(o) - ref).max() <= TOL_FP8_ABS
+    assert_rel_rows(to_f32(o), ref, TOL_BF16_REL, "paged fp8 vs twin")
     assert np.abs(to_f32(lse) - tl).max() <= TOL_LSE_ABS
 
 
@@ -225,6 +232,7 @@ def test_paged_fp8_ragged_empty_and_bad_table(ops, ps):
                                      v_scales=vps.cpu().numpy())
         ref = oracle.decode(to, oracle.BF16)
         assert np.abs(to_f32(o) - ref).max() <= TOL_FP8_ABS
+        assert_rel_rows(to_f32(o), ref, TOL_BF16_REL, f"paged fp8 ragged page={ps} vs twin")
         assert (to_f32(o[1]) == 0).all() and torch.isinf(lse[1]).all() and (lse[1] < 0).all()
         fin = np.isfinite(tl)
         assert np.array_equal(fin, torch.isfinite(lse).cpu().numpy())

@@ -5,14 +5,15 @@ tests/golden/make_golden.py independently of the oracle and the library.
 Tolerances: fp32 1e-5 relative; f16 1e-3 absolute (the reference's own
 functional-test bound, tests/test_translators.py:143 in Evan-Zhao/mlir-toy);
 bf16 2e-2 absolute (and 2e-2 relative to max|ref| for decode, whose outputs
-are small); fp8 KV 6e-2 end to end; scan 2e-2 * max(1, |ref|); LSE 1e-3.
+are small); fp8 KV 6e-2 end to end, absolute and relative to max|ref|; scan 2e-2 * max(1, |ref|); LSE 1e-3.
 """
 
 import numpy as np
 import pytest
 import torch
 
-from helpers import TOL_BF16_ABS, TOL_F32_REL, TOL_FP8_ABS, TOL_LSE_ABS, from_bf16_bits, to_f32
+from helpers import (TOL_BF16_ABS, TOL_BF16_REL, TOL_F32_REL, TOL_FP8_ABS, TOL_FP8_REL,
+                     TOL_LSE_ABS, assert_rel_rows, from_bf16_bits, to_f32)
 from test_golden import load, rel_err
 
 pytestmark = pytest.mark.gpu
@@ -59,7 +60,8 @@ def test_decode_golden(ops):
                                num_splits=int(g["num_splits"]), return_lse=True)
     torch.cuda.synchronize()
     err = np.abs(to_f32(o).astype(np.float64) - g["o"]).max()
-    assert err <= TOL_BF16_ABS and err <= 2e-2 * np.abs(g["o"]).max()
+    assert err <= TOL_BF16_ABS
+    assert_rel_rows(to_f32(o), g["o"], TOL_BF16_REL, "golden bf16 decode")
     assert np.abs(to_f32(lse) - g["lse"]).max() <= TOL_LSE_ABS
 
 
@@ -84,8 +86,10 @@ def test_decode_fp8_golden(ops):
     torch.cuda.synchronize()
     got = to_f32(o).astype(np.float64)
     err = np.abs(got - g["o"]).max()
-    assert err <= TOL_BF16_ABS and err <= 2e-2 * np.abs(g["o"]).max()
+    assert err <= TOL_BF16_ABS
+    assert_rel_rows(got, g["o"], TOL_BF16_REL, "golden fp8 decode vs same codes")
     assert np.abs(got - g["o_bf16_kv"]).max() <= TOL_FP8_ABS
+    assert_rel_rows(got, g["o_bf16_kv"], TOL_FP8_REL, "golden fp8 decode vs bf16 KV")
     assert np.abs(to_f32(lse) - g["lse"]).max() <= TOL_LSE_ABS
 
 

@@ -2,8 +2,9 @@
 
 A serving loop captures its decode step (or prefill) once and replays it.
 Every entry point here only launches kernels: no memset, no allocation, no
-synchronisation, and the one-time host set-up (kernel attributes, the static
-scratch address) happens on the first call, which runs before the capture.
+synchronisation, and the one-time host set-up (the static scratch address of
+the allocation-free entry point) happens on the first call, which runs
+before the capture.
 So each replay must equal an eager call on the same inputs bit for bit.
 Each test replays three times, rewriting the inputs in place before each
 replay and running eager work of another shape between replays, and checks

@@ -16,6 +16,11 @@ in the block table was written by ``v_readfirstlane`` two instructions
 before the copy that read it. The copy saw the previous base and loaded
 another step's tokens, with no fault.
 
+The fp8 decode's K-code register loads are inline assembly as well: the
+compiled code is checked for the order its waits rely on (each step's four K
+loads followed by its four V copies, and every wait before a K buffer is read
+leaving only the step's V copies and whole later steps in flight).
+
 The same compiled code also holds the kernels to the register budgets their
 speed depends on (test_kernel_register_budgets): the selective scan's
 output kernel within 96 VGPRs (five waves per SIMD), the production prefill
@@ -144,6 +149,94 @@ def kload_findings(asm: str) -> tuple[int, list[str]]:
     return waits, found
 
 
+VMEM = ("global_", "buffer_", "flat_", "scratch_")
+R8P = 4  # decode_partial_ring8: 32-token steps in flight (K buffers, V ring slots)
+
+
+def kload_order_findings(asm: str, in_flight: int = R8P) -> list[str]:
+    """The order the fp8 decode's waits rely on, per kernel with K-load waits.
+
+    * Issue: each step is four K loads followed at once by the four LDS copies
+      of its V tile, so 4 + 8 l vector-memory operations are issued after a
+      K buffer's last load when l later steps follow it.
+    * Wait: each s_waitcnt vmcnt(N) between a kload_wait and the vector-memory
+      operation before it is one of the kernel's per-`later` choices,
+      N = 4 + 8 l with 0 <= l < in_flight (the step's own V copies plus l
+      later steps may stay in flight), and each of those in_flight choices
+      occurs. That a wait never exceeds the operations actually issued after
+      the buffer then rests on l counting the later steps issued (the
+      kernel's `later`), which every ragged-length parity case exercises.
+    Operations of other kinds issued in between only make a wait retire the
+    K loads earlier. Returns the findings."""
+    found = []
+    allowed = {4 + 8 * l for l in range(in_flight)}
+    for name, body in re.findall(r"^(\S+):\s*;\s*@\S+\n(.*?)^\.Lfunc_end", asm, re.S | re.M):
+        if "kload_wait" not in body:
+            continue
+        seq = []  # ("K" | "C" | "M" other memory | "W" | "N" wait, vmcnt)
+        for line in body.splitlines():
+            t = line.strip()
+            if t.startswith(VMEM):
+                m = t.split()[0]
+                if KLOAD.match(line):
+                    seq.append(("K", None))
+                else:
+                    seq.append(("C" if m.startswith("global_load_lds") else "M", None))
+            elif "kload_wait" in t:
+                seq.append(("W", None))
+            elif t.startswith("s_waitcnt") and "vmcnt(" in t:
+                seq.append(("N", int(re.search(r"vmcnt\((\d+)\)", t).group(1))))
+        mem = [k for k, _ in seq if k in "KCM"]
+        i = 0
+        while i < len(mem):
+            if mem[i] != "K":
+                i += 1
+                continue
+            j = i
+            while j < len(mem) and mem[j] == "K":
+                j += 1
+            c = j
+            while c < len(mem) and mem[c] == "C":
+                c += 1
+            if j - i != 4 or c - j != 4:
+                found.append(f"{name}: a step issues {j - i} K loads then {c - j} LDS copies "
+                             f"(want 4 and 4)")
+            i = c
+        seen = set()
+        for w, (kind, _) in enumerate(seq):
+            if kind != "W":
+                continue
+            k = w - 1
+            while k >= 0 and seq[k][0] == "N":
+                n = seq[k][1]
+                seen.add(n)
+                if n not in allowed:
+                    found.append(f"{name}: vmcnt({n}) before a kload_wait is not one of "
+                                 f"{sorted(allowed)}")
+                k -= 1
+            if k == w - 1:
+                found.append(f"{name}: a kload_wait with no vmcnt wait after the last load")
+        if seen != allowed:
+            found.append(f"{name}: waits before kload_wait {sorted(seen)}, want {sorted(allowed)}")
+    return found
+
+
+def test_kload_order_checker():
+    step = ("\tglobal_load_dwordx4 v[18:21], v140, s[20:21] nt\n" * 4
+            + "\tglobal_load_lds_dwordx4 v61, s[36:37] nt\n" * 4)
+    waits = "".join(f"\ts_waitcnt vmcnt({n})\n" for n in (28, 20, 12, 4))
+    good = ("k:  ; @k\n" + step * 4 + waits
+            + "\t; kload_wait v[18:21] v[22:25] v[26:29] v[30:33]\n.Lfunc_end0:\n")
+    assert kload_order_findings(good) == []
+    assert len(kload_order_findings(good.replace("vmcnt(12)", "vmcnt(13)"))) == 2
+    assert kload_order_findings(good.replace("vmcnt(28)", "vmcnt(36)"))
+    short = good.replace(step, step.replace("\tglobal_load_lds_dwordx4 v61, s[36:37] nt\n", "", 1), 1)
+    assert kload_order_findings(short)
+    late = good.replace(step, step.replace("nt\n\tglobal_load_lds", "nt\n\tglobal_load_dword v1, "
+                                           "v[2:3], off\n\tglobal_load_lds", 1), 1)
+    assert kload_order_findings(late)
+
+
 def test_kload_checker_flags_a_copy():
     ok = ("k:  ; @k\n\tglobal_load_dwordx4 v[18:21], v140, s[20:21] nt\n"
           "\t; kload_wait v[18:21] v[22:25] v[26:29] v[30:33]\n.Lfunc_end0:\n")
@@ -201,6 +294,7 @@ def test_lds_dma_wait_states(compiled):
         n, found = kload_findings(asm)
         kwaits += n
         report += [f"{name}: {f}" for f in found]
+        report += [f"{name}: {f}" for f in kload_order_findings(asm)]
     assert copies > 0, "no LDS DMA copies found: the checker is looking at the wrong code"
     assert kwaits > 0, "no K-load waits found: the checker is looking at the wrong code"
     assert not report, "\n".join(report)
