@@ -7,8 +7,11 @@ per-row logsumexp, inputs ~ 0.5 N(0,1) resident in HBM. A step is one
 neptune_attn_fwd launch over that batch. The JSON line also carries, under
 "secondary", the split-K GQA decode (bf16 and fp8 KV, contiguous and paged)
 and selective-scan configurations measured the same way (GB/s against HBM),
-and config 1 (fp32 single-head attention, latency-bound, TFLOP/s), each with
-its own cpu_baseline.
+config 1 (fp32 single-head attention, latency-bound, TFLOP/s) and the
+reference's own tile program (f16 non-causal [1, 32, 4096, 128] through the
+HTile front end), each with its own cpu_baseline, and a bf16 GEMM
+(hipBLASLt) that calibrates the dense MFMA rate this box sustains: the
+headline's prefill_over_gemm is the prefill's rate over that GEMM's.
 
 Each workload first runs untimed for SPINUP_S seconds (so the GPU is at its
 working clocks), then W warmup steps, then exactly K timed steps.
@@ -144,6 +147,52 @@ def bench_prefill(ops, torch, steps, warmup, B=4, H=32, S=4096, D=128):
     wall, ev = time_launches(step, steps, warmup)
     flops = prefill_flops(B, H, S, D)
     return {"q": q, "k": k, "v": v, "wall": wall, "event_s": ev, "flops": flops}
+
+
+def bench_htile_reference(torch, steps, warmup, B=1, H=32, S=4096, D=128):
+    """The reference's own tile program: the flash-attention HTile program
+    (f16, non-causal MHA [1, 32, 4096, 128], 128-row query blocks, 64-key
+    blocks, pipeline_stages 2) bound by this backend's HTile front end
+    (neptune_hip.htile.translate_source) and launched as the reference's
+    functional test launches the generated kernel,
+    flash_attention_htile[(32, 32, 1)](q, k, v, out)
+    (tests/test_translators.py:184-194). The program text comes from
+    tests/htile_gen.py, which writes it for a given shape and dtype."""
+    if str(ROOT / "tests") not in sys.path:
+        sys.path.insert(0, str(ROOT / "tests"))
+    from htile_gen import program
+
+    from neptune_hip import htile
+
+    kern = htile.translate_source(program(B=B, H=H, S=S, D=D, dtype="f16")).flash_attention_htile
+    grid = kern.program.grid
+    g = torch.Generator(device="cuda").manual_seed(6)
+    q, k, v = (torch.randn((B, H, S, D), device="cuda", generator=g).to(torch.float16)
+               for _ in range(3))
+    out = torch.empty_like(q)
+    launch = kern[grid]
+    wall, ev = time_launches(lambda _: launch(q, k, v, out), steps, warmup)
+    flops = 4.0 * B * H * S * S * D  # every (query, key) pair: two GEMMs of 2 D FLOPs
+    name = (f"reference tile program flash_attention_htile f16 [{B},{H},{S},{D}] non-causal, "
+            f"grid {grid} via htile.translate_source")
+
+    def cpu(budget_s):
+        """The oracle (HTile policy) on whole heads of the same inputs."""
+        import oracle
+
+        per_head = flops / (B * H)
+
+        def run(i):
+            b, h = divmod(i, H)
+            qs, ks, vs = (_host_bits(t[b:b + 1, h:h + 1]) for t in (q, k, v))
+            t0 = time.perf_counter()
+            oracle.attn_fwd(qs, ks, vs, oracle.F16)
+            return time.perf_counter() - t0
+
+        return _cpu_sample(run, B * H, per_head, "TFLOP/s", 1e12, budget_s,
+                           "heads of the same tile-program attention")
+
+    return name, wall, ev, flops, cpu
 
 
 def bench_decode(ops, torch, steps, warmup, fp8):
@@ -382,6 +431,10 @@ def cpu_baseline_prefill(res, budget_s=15.0, max_slices=64):
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.txt"
+# roofline.traffic is not measured by this run: it is the byte count of a
+# separate rocprofv3 counter pass, summarised in that file
+TRAFFIC_SOURCE = ("profiles/hbm_traffic.txt: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes "
+                  "over the same workload, scaled by a 1 GiB copy's counts; not this run")
 
 
 def measured_traffic():
@@ -410,7 +463,8 @@ def bench_gemm(torch, steps, warmup, n=8192):
     """A bf16 n^3 GEMM through torch.matmul (hipBLASLt): the vendor's own dense
     MFMA rate on this box, under the same power cap as the prefill. It
     calibrates what fraction of the nominal MFMA peak dense bf16 work reaches
-    here; not part of the default run."""
+    here; the default run carries it as a secondary entry and puts the
+    prefill's rate over it on the headline (prefill_over_gemm)."""
     a = torch.randn((n, n), device="cuda").to(torch.bfloat16)
     b = torch.randn((n, n), device="cuda").to(torch.bfloat16)
     c = torch.empty((n, n), device="cuda", dtype=torch.bfloat16)
@@ -418,7 +472,8 @@ def bench_gemm(torch, steps, warmup, n=8192):
     return f"bf16 GEMM {n}^3 (torch.matmul, hipBLASLt)", wall, ev, 2.0 * n ** 3, None
 
 
-def mfma_entry(name, wall, ev, flops, steps):
+def mfma_entry(name, wall, ev, flops, steps, cpu=None):
+    """A 16-bit MFMA-bound workload (the same dense peak for f16 and bf16)."""
     tf = flops / ev / 1e12
     return {
         "workload": name,
@@ -427,6 +482,7 @@ def mfma_entry(name, wall, ev, flops, steps):
         "us_per_step": round(ev * 1e6, 2),
         "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None},
+        "cpu_baseline": cpu,
     }
 
 
@@ -439,7 +495,8 @@ def hbm_entry(key, name, wall, ev, nbytes, steps, traffic, cpu=None):
         "us_per_step": round(ev * 1e6, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                     "traffic": traffic.get(key)},
+                     "traffic": traffic.get(key),
+                     "traffic_source": TRAFFIC_SOURCE if key in traffic else None},
         "cpu_baseline": cpu,
     }
 
@@ -489,7 +546,8 @@ def main():
                     help="skip the decode/scan configurations")
     ap.add_argument("--workload", default="all",
                     choices=["all", "prefill", "decode", "decode_fp8", "decode_paged",
-                             "decode_paged_fp8", "scan", "config1", "copy", "gemm"],
+                             "decode_paged_fp8", "scan", "config1", "copy", "gemm",
+                             "htile_ref"],
                     help="run one configuration only (for profiling); 'copy' is a plain "
                          "1 GiB device copy used to calibrate HBM byte counters, 'gemm' a "
                          "bf16 8192^3 torch.matmul that calibrates the dense MFMA rate")
@@ -533,12 +591,13 @@ def main():
         "copy": lambda: bench_copy(torch, args.steps, args.warmup),
         "gemm": lambda: bench_gemm(torch, args.steps, args.warmup),
         "config1": lambda: bench_config1(ops, torch, args.steps, args.warmup),
+        "htile_ref": lambda: bench_htile_reference(torch, args.steps, args.warmup),
     }
     if args.workload in single:
         name, wall, ev, work, cpu = single[args.workload]()
         if args.workload == "config1":
             entry = config1_entry(name, wall, ev, work, args.steps)
-        elif args.workload == "gemm":
+        elif args.workload in ("gemm", "htile_ref"):
             entry = mfma_entry(name, wall, ev, work, args.steps)
         else:
             entry = hbm_entry(args.workload, name, wall, ev, work, args.steps, traffic)
@@ -554,6 +613,7 @@ def main():
           file=sys.stderr, flush=True)
 
     secondary = []
+    gemm_tf = None
     if not args.no_secondary and args.workload == "all":
         del res["k"], res["v"]
         torch.cuda.empty_cache()
@@ -566,10 +626,18 @@ def main():
                         ("decode_paged_fp8", lambda: bench_decode_paged(ops, torch, sec_steps,
                                                                         sec_warm, fp8=True)),
                         ("scan", lambda: bench_scan(ops, torch, sec_steps, sec_warm)),
-                        ("config1", lambda: bench_config1(ops, torch, sec_steps, sec_warm))):
+                        ("config1", lambda: bench_config1(ops, torch, sec_steps, sec_warm)),
+                        ("htile_ref", lambda: bench_htile_reference(torch, sec_steps, sec_warm)),
+                        ("gemm", lambda: bench_gemm(torch, sec_steps, sec_warm))):
             name, wall, ev, work, cpu_fn = fn()
-            cpu = None if args.no_cpu else cpu_fn(CPU_BUDGET_S)
-            if key == "config1":  # wall and ev are per launch: steps x launches per graph
+            cpu = None if (args.no_cpu or cpu_fn is None) else cpu_fn(CPU_BUDGET_S)
+            if key in ("htile_ref", "gemm"):
+                secondary.append(mfma_entry(name, wall, ev, work, sec_steps, cpu))
+                if key == "gemm":
+                    gemm_tf = work / ev / 1e12
+                print(f"# {name}: {ev * 1e6:.1f} us, {work / ev / 1e12:.1f} TFLOP/s",
+                      file=sys.stderr, flush=True)
+            elif key == "config1":  # wall and ev are per launch: steps x launches per graph
                 secondary.append(config1_entry(name, wall, ev, work, sec_steps, cpu))
                 print(f"# {name}: {ev * 1e6:.1f} us, {work / ev / 1e12:.3f} TFLOP/s",
                       file=sys.stderr, flush=True)
@@ -588,6 +656,13 @@ def main():
             for _ in range(3))
 
     cpu = None if args.no_cpu else cpu_baseline_prefill(res)
+    # the prefill's rate over the vendor GEMM's, both timed in this run: how
+    # close the fused attention (softmax included) comes to dense bf16 MFMA
+    # work under the same power cap
+    prefill_over_gemm = None if gemm_tf is None else {
+        "ratio": round(achieved / gemm_tf, 4), "gemm_achieved": round(gemm_tf, 1),
+        "gemm_frac": round(gemm_tf / PEAK_BF16_TFLOPS, 4), "unit": "TFLOP/s",
+        "gemm": "bf16 8192^3 torch.matmul (hipBLASLt), secondary entry 'gemm'"}
 
     line = {
         "metric": METRIC,
@@ -610,7 +685,9 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": traffic.get("prefill")},
+                     "traffic": traffic.get("prefill"),
+                     "traffic_source": TRAFFIC_SOURCE if "prefill" in traffic else None},
+        "prefill_over_gemm": prefill_over_gemm,
         "cpu_baseline": cpu,
         "secondary": secondary,
     }
