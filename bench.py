@@ -433,14 +433,16 @@ def cpu_baseline_prefill(res, budget_s=15.0, max_slices=64):
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.txt"
 # roofline.traffic is not measured by this run: it is the byte count of a
 # separate rocprofv3 counter pass, summarised in that file
-TRAFFIC_SOURCE = ("profiles/hbm_traffic.txt: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes "
+TRAFFIC_SOURCE = ("profiles/hbm_traffic.txt: L2 fetch and write bytes to the data fabric (HBM or "
+                  "the MALL in front of it) from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes "
                   "over the same workload, scaled by a 1 GiB copy's counts; not this run")
 
 
 def measured_traffic():
-    """HBM bytes per launch per workload, from the rocprofv3 FETCH_SIZE /
-    WRITE_SIZE passes summarised in profiles/hbm_traffic.txt (lines
-    'workload bytes'); {} when that summary is absent."""
+    """Bytes per launch between L2 and the data fabric (HBM, or the MALL in
+    front of it) per workload, from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+    passes summarised in profiles/hbm_traffic.txt (lines 'workload bytes');
+    {} when that summary is absent."""
     out = {}
     if TRAFFIC_FILE.is_file():
         for line in TRAFFIC_FILE.read_text().splitlines():
@@ -515,6 +517,20 @@ def config1_entry(name, wall, ev, flops, steps, cpu=None):
     }
 
 
+def short_kernel_name(name):
+    """A kernel name without its namespaces, return type and argument list,
+    template arguments kept (they tell the instantiations apart)."""
+    n = name.replace("void ", "").replace("(anonymous namespace)::", "").replace("neptune::", "")
+    depth = 0
+    for i, ch in enumerate(n):
+        depth += ch == "<"
+        depth -= ch == ">"
+        if ch == "(" and depth == 0:
+            n = n[:i]
+            break
+    return n[:90]
+
+
 def trace_summary(path, last):
     """Markdown table of a rocprofv3 kernel-trace CSV: per kernel, every
     launch, and the last `last` launches alone (the timed steps of a
@@ -532,7 +548,7 @@ def trace_summary(path, last):
         rs.sort()
         tail = [d / 1e3 for _, d in rs[-last:]]
         allv = sum(d for _, d in rs) / len(rs) / 1e3
-        print(f"| `{name[:60]}` | {len(rs)} | {allv:.1f} | {sum(tail) / len(tail):.1f} | "
+        print(f"| `{short_kernel_name(name)}` | {len(rs)} | {allv:.1f} | {sum(tail) / len(tail):.1f} | "
               f"{min(tail):.1f} | {max(tail):.1f} |")
 
 
