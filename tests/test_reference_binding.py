@@ -1,6 +1,5 @@
 """CPU tests of the reference-side binding (mlir-toy_amd/reference_binding/hip.py),
-the module INTEGRATION.md tells a maintainer of the reference to add as
-src/neptune_mlir/backends/hip.py.
+the module a maintainer of the reference adds as src/neptune_mlir/backends/hip.py.
 
 * The torch dtype reaches the descriptor by equality: float16 -> F16,
   bfloat16 -> BF16, float32 -> F32 (str(torch.bfloat16) also ends in
