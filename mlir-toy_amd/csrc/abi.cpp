@@ -220,16 +220,15 @@ neptune_status neptune_decode_workspace_bytes(const neptune_decode_desc *d, size
 
 namespace {
 // shared tail of the decode entry points (pk != nullptr: paged KV;
-// workspace == kStaticScratch: the library's static device scratch)
-void *const kStaticScratch = reinterpret_cast<void *>(~uintptr_t(0));
-
+// scratch: the partials go to the library's static device scratch, and
+// workspace / workspace_bytes are not used)
 neptune_status decode_run(const neptune_decode_desc *d, const neptune_paged_kv_desc *pk,
                           const void *q, const void *k, const void *v, const float *k_scale,
                           const float *v_scale, const int32_t *block_table,
-                          const int32_t *seq_lens, void *o, float *lse, void *workspace,
-                          size_t workspace_bytes, void *stream) {
-  if (!workspace) return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode: workspace is NULL");
-  const bool scratch = workspace == kStaticScratch;
+                          const int32_t *seq_lens, void *o, float *lse, bool scratch,
+                          void *workspace, size_t workspace_bytes, void *stream) {
+  if (!scratch && !workspace)
+    return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode: workspace is NULL");
   int64_t splits, chunk;
   decode_layout(d, &splits, &chunk);
   const size_t need = decode_ws_bytes(d, splits);
@@ -293,8 +292,8 @@ neptune_status neptune_decode_splitk(const neptune_decode_desc *d, const void *q
   const bool fp8 = d->kv_dtype == NEPTUNE_DTYPE_FP8_E4M3;
   if (fp8 && (!k_scale || !v_scale))
     return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode: fp8 KV needs k_scale and v_scale");
-  return decode_run(d, nullptr, q, k, v, k_scale, v_scale, nullptr, nullptr, o, lse, workspace,
-                    workspace_bytes, stream);
+  return decode_run(d, nullptr, q, k, v, k_scale, v_scale, nullptr, nullptr, o, lse, false,
+                    workspace, workspace_bytes, stream);
 }
 
 neptune_status neptune_decode_splitk_noalloc(const neptune_decode_desc *d, const void *q,
@@ -307,8 +306,8 @@ neptune_status neptune_decode_splitk_noalloc(const neptune_decode_desc *d, const
     return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode_noalloc: q, k, v and o must be non-NULL");
   if (d->kv_dtype == NEPTUNE_DTYPE_FP8_E4M3 && (!k_scale || !v_scale))
     return fail(NEPTUNE_ERR_INVALID_ARGUMENT, "decode_noalloc: fp8 KV needs k_scale and v_scale");
-  return decode_run(d, nullptr, q, k, v, k_scale, v_scale, nullptr, nullptr, o, lse,
-                    kStaticScratch, 0, stream);
+  return decode_run(d, nullptr, q, k, v, k_scale, v_scale, nullptr, nullptr, o, lse, true,
+                    nullptr, 0, stream);
 }
 
 namespace {
@@ -354,7 +353,7 @@ neptune_status neptune_decode_paged(const neptune_decode_desc *d, const neptune_
     return fail(NEPTUNE_ERR_UNSUPPORTED,
                 "decode_paged: kv_dtype must be BF16 (fp8 pools: neptune_decode_paged_fp8)");
   return decode_run(d, pk, q, k_pages, v_pages, nullptr, nullptr, block_table, seq_lens, o, lse,
-                    workspace, workspace_bytes, stream);
+                    false, workspace, workspace_bytes, stream);
 }
 
 neptune_status neptune_decode_paged_fp8(const neptune_decode_desc *d,
@@ -380,7 +379,7 @@ neptune_status neptune_decode_paged_fp8(const neptune_decode_desc *d,
   neptune_decode_desc dd = *d;
   dd.scale_block = pk->page_size;
   return decode_run(&dd, pk, q, k_pages, v_pages, k_scales, v_scales, block_table, seq_lens, o,
-                    lse, workspace, workspace_bytes, stream);
+                    lse, false, workspace, workspace_bytes, stream);
 }
 
 neptune_status neptune_kv_quantize_fp8(int64_t batch, int64_t heads_kv, int64_t seq_kv,

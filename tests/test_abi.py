@@ -269,6 +269,20 @@ def test_decode_workspace_and_fp8_errors(lib):
     assert _decode(lib, _dec_desc(), ptrs=(FAKE, FAKE, 0)) == _abi.ERR_INVALID_ARGUMENT
 
 
+@pytest.mark.parametrize("ws,ws_bytes,status", [
+    (None, 1 << 30, _abi.ERR_INVALID_ARGUMENT),
+    # any pointer value is a caller's workspace: its size is checked, and the
+    # library's static scratch is reached only through the noalloc entry point
+    ((1 << 64) - 1, 0, _abi.ERR_WORKSPACE_TOO_SMALL),
+    ((1 << 64) - 16, 16, _abi.ERR_WORKSPACE_TOO_SMALL),
+])
+def test_decode_workspace_pointer_is_the_callers(lib, ws, ws_bytes, status):
+    d = _dec_desc()
+    assert lib.neptune_decode_splitk(ctypes.byref(d), FAKE, FAKE, FAKE, None, None, FAKE, None, ws,
+                                     ws_bytes, None) == status
+    assert lib.neptune_last_error()
+
+
 def _pages(**kw):
     p = _abi.PagedKvDesc()
     p.num_pages, p.page_size, p.max_pages = 64, 64, 32
