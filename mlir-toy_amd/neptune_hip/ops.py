@@ -28,6 +28,12 @@ def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
+def _check_workspace(workspace: torch.Tensor | None) -> None:
+    # the library writes numel * element_size bytes from data_ptr
+    if workspace is not None and not workspace.is_contiguous():
+        raise ValueError("workspace must be a contiguous tensor")
+
+
 def _require_cuda(*tensors: torch.Tensor) -> None:
     dev = None
     for t in tensors:
@@ -81,7 +87,7 @@ def attention(
     """
     if scale is not None and scale_log2 is not None:
         raise ValueError("give scale or scale_log2, not both")
-    _require_cuda(q, k, v, out)
+    _require_cuda(q, k, v, out, lse)
     if q.dtype not in _TORCH_TO_DTYPE or k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError(f"q, k, v must share one of {list(_TORCH_TO_DTYPE)}")
     B, Hq, Sq, D = q.shape
@@ -212,6 +218,7 @@ def decode_splitk(
     elif k_scale is not None or v_scale is not None:
         raise ValueError("k_scale / v_scale apply to E4M3 KV only")
     _require_cuda(q3, k, v, k_scale, v_scale, workspace)
+    _check_workspace(workspace)
     desc = _decode_desc(q3, k, num_splits, scale_block, scale,
                         _abi.DTYPE_FP8_E4M3 if fp8 else _abi.DTYPE_BF16)
     lib = load_library()
@@ -292,6 +299,7 @@ def decode_paged(
     if block_table.dim() != 2 or block_table.shape[0] != B or tuple(seq_lens.shape) != (B,):
         raise ValueError("block_table [B, max_pages] and seq_lens [B] must match q's batch")
     _require_cuda(q3, k_pages, v_pages, block_table, seq_lens, workspace, k_scales, v_scales)
+    _check_workspace(workspace)
     max_pages = block_table.shape[1]
     L = int(max_seq_len) if max_seq_len is not None else max_pages * psize
     k4 = torch.empty((B, Hk, L, D), dtype=k_pages.dtype, device="meta")

@@ -66,10 +66,32 @@ def _dtype(t):
         raise NotImplementedError(f"flash_attention_htile: no kernel for {t.dtype}") from None
 
 
+def _check(q, k, v, out):
+    """What the generated kernel assumes of its arguments, checked before any
+    call: one device (the GPU whenever there is one), one dtype, agreeing
+    [batch, heads, seq, head_dim] shapes, and contiguous storage (the zero
+    strides the descriptor carries)."""
+    ts = (q, k, v, out)
+    if len({t.device for t in ts}) != 1:
+        raise RuntimeError("flash_attention_htile: q, k, v and out must be on one device")
+    if not q.is_cuda and torch.cuda.is_available():
+        raise RuntimeError("flash_attention_htile: q, k, v and out must be GPU tensors")
+    if any(t.dtype != q.dtype for t in ts):
+        raise RuntimeError("flash_attention_htile: q, k, v and out must share one dtype")
+    if (q.dim() != 4 or k.dim() != 4 or tuple(v.shape) != tuple(k.shape)
+            or tuple(out.shape) != tuple(q.shape)
+            or (k.shape[0], k.shape[3]) != (q.shape[0], q.shape[3])):
+        raise RuntimeError(f"flash_attention_htile: shapes q {tuple(q.shape)} k {tuple(k.shape)} "
+                           f"v {tuple(v.shape)} out {tuple(out.shape)} do not agree")
+    if not all(t.is_contiguous() for t in ts):
+        raise NotImplementedError("flash_attention_htile: contiguous tensors only")
+
+
 def flash_attention_htile(q, k, v, out):
     """Same arguments and effect as the generated kernel: out <- attention(q,
     k, v) over contiguous [batch, heads, seq, head_dim] tensors, scaled by
     log2(e)/sqrt(head_dim) in the exp2 domain (the HTile constant)."""
+    _check(q, k, v, out)
     lib = _lib if _lib is not None else load()
     d = AttnDesc()
     d.batch, d.heads_q, d.seq_q, d.head_dim = q.shape

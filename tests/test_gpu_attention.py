@@ -202,6 +202,14 @@ def test_q_zero_gives_prefix_mean(ops):
     assert max_abs(to_f32(out), prefix.numpy()) <= TOL_BF16_ABS
 
 
+def test_host_lse_raises(ops):
+    """A caller's lse in host memory is refused before any launch."""
+    q = torch.zeros((1, 1, 64, 128), dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty((1, 1, 64), dtype=torch.float32)
+    with pytest.raises(ValueError):
+        ops.attention(q, q, q, lse=lse)
+
+
 def test_unsupported_head_dim_raises(ops):
     from neptune_hip import NeptuneUnsupported
     q = torch.zeros((1, 1, 64, 96), dtype=torch.bfloat16, device="cuda")

@@ -244,6 +244,17 @@ def test_workspace_too_small(ops):
         ops.decode_splitk(q, k, k, workspace=ws)
 
 
+def test_strided_workspace_raises(ops):
+    """The library writes the workspace's numel * element_size bytes from its
+    first element, so a strided view is refused before any launch."""
+    q = torch.zeros((1, 4, 128), dtype=torch.bfloat16, device="cuda")
+    k = torch.zeros((1, 1, 256, 128), dtype=torch.bfloat16, device="cuda")
+    n = ops.decode_workspace_bytes(q, k)
+    ws = torch.empty(2 * n, dtype=torch.uint8, device="cuda")[::2]
+    with pytest.raises(ValueError):
+        ops.decode_splitk(q, k, k, workspace=ws)
+
+
 
 SEG_STEP = 4.0  # V's step per 2^24 tokens (4 GiB of 256-byte rows)
 

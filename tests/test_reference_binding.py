@@ -5,6 +5,8 @@ the module a maintainer of the reference adds as src/neptune_mlir/backends/hip.p
   bfloat16 -> BF16, float32 -> F32 (str(torch.bfloat16) also ends in
   "float16", so a suffix test would bind bf16 as F16); other dtypes raise
   NotImplementedError before any call.
+* Arguments that break what the generated kernel assumes (one device, one
+  dtype, agreeing shapes, contiguous storage) are refused before any call.
 * Through the real library's validation path (no device here), a shape the
   fp32 kernel covers and the 16-bit kernels do not (head_dim 32) is accepted
   for F32 (and then finds no device: RuntimeError) and refused as
@@ -78,6 +80,21 @@ def test_header_enum_values():
 def test_unsupported_dtype_raises_before_the_call(recorder, dtype):
     with pytest.raises(NotImplementedError):
         hip.flash_attention_htile(*_qkvo(dtype))
+    assert recorder.seen == []
+
+
+def test_mismatched_arguments_raise_before_the_call(recorder):
+    q, k, v, o = _qkvo(torch.float16)
+    bad = [
+        ((q, k, v, torch.empty((1, 2, 8, 64), dtype=torch.float16)), RuntimeError),  # out shape
+        ((q, k, v[:, :, :16], o), RuntimeError),                                  # v != k
+        ((q, k.float(), v, o), RuntimeError),                                     # dtypes
+        ((q.transpose(2, 3).contiguous().transpose(2, 3), k, v, o),               # strided q
+         NotImplementedError),
+    ]
+    for args, exc in bad:
+        with pytest.raises(exc):
+            hip.flash_attention_htile(*args)
     assert recorder.seen == []
 
 
