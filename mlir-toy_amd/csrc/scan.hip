@@ -282,10 +282,13 @@ __device__ inline __amdgpu_buffer_rsrc_t byte_range(const void *base, uint32_t b
 constexpr uint32_t kDropped = 0x80000000u;
 
 // The single pass (kScanFull), and the output pass of the chunked path;
-// SOFTPLUS and GATE (z given) are fixed per launch. Five work-groups per CU
-// (at most 96 VGPRs): what config 4's 1280 work-groups need to run in one
-// round.
-template <int MODE, bool SOFTPLUS, bool GATE>
+// SOFTPLUS and GATE (z given) are fixed per launch, and so is PAIRS: B and C
+// come in 4-byte step pairs (even seq_len, 4-byte aligned rows), so each
+// stage lane fetches its two steps of B and of C with one dword load each
+// (a chunk's loads are 8 rather than 10; measured 2% faster at config 4).
+// Five work-groups per CU (at most 96 VGPRs): what config 4's 1280
+// work-groups need to run in one round.
+template <int MODE, bool SOFTPLUS, bool GATE, bool PAIRS>
 __global__ __launch_bounds__(NT, 5) void selective_scan_out(ScanArgs a) {
   static_assert(MODE == kScanFull || MODE == kScanOutput, "output kernel modes");
   __shared__ __attribute__((aligned(16))) float xs[4][TT / 2][XR];    // [wave][step][lane]
@@ -352,8 +355,14 @@ __global__ __launch_bounds__(NT, 5) void selective_scan_out(ScanArgs a) {
       fdr[set][i] = __builtin_amdgcn_raw_buffer_load_b16(rdr, vo + 32 * i, 0, 0);
       if constexpr (GATE)
         fz[set][i] = __builtin_amdgcn_raw_buffer_load_b16(rz, vo + 32 * i, 0, 0);
-      fB[set][i] = __builtin_amdgcn_raw_buffer_load_b16(rB, vbc + 2 * i, 0, 0);
-      fC[set][i] = __builtin_amdgcn_raw_buffer_load_b16(rC, vbc + 2 * i, 0, 0);
+      if constexpr (!PAIRS) {
+        fB[set][i] = __builtin_amdgcn_raw_buffer_load_b16(rB, vbc + 2 * i, 0, 0);
+        fC[set][i] = __builtin_amdgcn_raw_buffer_load_b16(rC, vbc + 2 * i, 0, 0);
+      }
+    }
+    if constexpr (PAIRS) {  // steps 2 sp and 2 sp + 1 in one dword
+      fB[set][0] = __builtin_amdgcn_raw_buffer_load_b32(rB, vbc, 0, 0);
+      fC[set][0] = __builtin_amdgcn_raw_buffer_load_b32(rC, vbc, 0, 0);
     }
   };
 
@@ -398,10 +407,14 @@ __global__ __launch_bounds__(NT, 5) void selective_scan_out(ScanArgs a) {
       ul[i] = uln2;
       gate[i] = GATE ? silu_fast(__uint_as_float(fz[par][i] << 16)) : 1.0f;
     }
-    *(float2 *)&bq[par][bn][2 * sp] =
-        make_float2(__uint_as_float(fB[par][0] << 16), __uint_as_float(fB[par][1] << 16));
-    cs[par][2 * sp][bn] = __uint_as_float(fC[par][0] << 16);
-    cs[par][2 * sp + 1][bn] = __uint_as_float(fC[par][1] << 16);
+    // step 2 sp + i of B or C: the high half of the pair's dword (PAIRS), or
+    // register i
+    auto bc = [&](const uint32_t(&r)[2], int i) {
+      return __uint_as_float(PAIRS ? (i ? r[0] & 0xffff0000u : r[0] << 16) : r[i] << 16);
+    };
+    *(float2 *)&bq[par][bn][2 * sp] = make_float2(bc(fB[par], 0), bc(fB[par], 1));
+    cs[par][2 * sp][bn] = bc(fC[par], 0);
+    cs[par][2 * sp + 1][bn] = bc(fC[par], 1);
     fetch(std::integral_constant<int, 1 - par>{}, t0 + TT);
     // B / C of this chunk are visible to every wave; cs[par] and bq[par]
     // are next written two chunks on, behind the next chunk's barrier,
@@ -631,8 +644,12 @@ hipError_t launch_selective_scan(const ScanLaunch &L, hipStream_t s) {
   // the output kernel for this mode and these options
   auto out = [&](auto mode, unsigned grid) {
     constexpr int M = decltype(mode)::value;
-    auto k = sp ? (gate ? selective_scan_out<M, true, true> : selective_scan_out<M, true, false>)
-                : (gate ? selective_scan_out<M, false, true> : selective_scan_out<M, false, false>);
+    auto pick = [&](auto PAIRS) {
+      constexpr bool P = decltype(PAIRS)::value;
+      return sp ? (gate ? selective_scan_out<M, true, true, P> : selective_scan_out<M, true, false, P>)
+                : (gate ? selective_scan_out<M, false, true, P> : selective_scan_out<M, false, false, P>);
+    };
+    auto k = a.vec ? pick(std::true_type{}) : pick(std::false_type{});
     hipLaunchKernelGGL(k, dim3(grid), dim3(NT), 0, s, a);
   };
   if (a.nch <= 1) {
