@@ -68,6 +68,22 @@ def test_scan_small_matches_oracle(ops, b, d, L, bias):
     _check(y, ins)
 
 
+def test_scan_pair_loads_equal_16bit_loads(ops):
+    """B and C taken as 4-byte step pairs (aligned inputs) and as 16-bit
+    values (B two bytes past a 4-byte boundary) give the same bits. The
+    shape has 1024 channel blocks, so both launches take the single pass."""
+    _log("case: scan pair loads against 16-bit loads b=4 d=4096 L=96")
+    u, dr, A, Bm, Cm, D, z, bias = (t.cuda() for t in scan_inputs(4, 4096, 96))
+    y_pairs = ops.selective_scan(u, dr, A, Bm, Cm, D, z, bias)
+    buf = torch.empty(Bm.numel() + 1, dtype=Bm.dtype, device=Bm.device)
+    b_odd = buf[1:].view(Bm.shape)
+    b_odd.copy_(Bm)
+    assert b_odd.data_ptr() % 4 == 2
+    y_16 = ops.selective_scan(u, dr, A, b_odd, Cm, D, z, bias)
+    torch.cuda.synchronize()
+    assert torch.equal(y_pairs.view(torch.int16), y_16.view(torch.int16))
+
+
 def test_scan_no_gate_no_D(ops):
     _log("case: scan without z and D")
     u, dr, A, Bm, Cm, D, z, bias = scan_inputs(1, 32, 256)
